@@ -1,0 +1,231 @@
+"""Benchmark of the fused rANS-decode + batch-1 GEMV on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+Workload: one down_proj-shaped (1536 x 8960) matrix of ECSQ-like integer
+codes, round(w/step) with w ~ Laplace(0,1) from default_rng(1536+8960) and
+one step chosen so the full tensor's empirical entropy is 3.25 bits, stored
+in the w64 rANS format; log-normal (sigma 0.5) per-column waterfilling steps;
+x ~ N(0,1) in bf16; batch 1.  A step is one GEMV y = codes @ (x*step).
+
+Timing: W warm-up launches, then K launches captured in one HIP graph (so
+Python dispatch cost is not measured) and replayed between HIP events on the
+launch stream.  Successive launches rotate over enough distinct encoded
+copies (>= 512 MB) that the 256 MB Infinity Cache and the L2 cannot serve the
+compressed stream; a hot-cache figure (one copy) is reported separately, as
+is torch's bf16 F.linear (rocBLAS/hipBLASLt) on the same shape and rotation.
+
+Prints one JSON line.  `value` is the bf16-equivalent effective weight
+throughput rows*cols*2 bytes / time per GEMV.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "vram-compression_amd"))
+import rans  # noqa: E402
+import rans_bench as B  # noqa: E402
+
+METRIC = "effective weight GB/s (bf16-equiv) + µs/GEMV at 1536x8960, 3.25 b/w"
+ROWS, COLS, BITS = 1536, 8960, 3.25
+HBM_PEAK_GBS = 8000.0
+ROTATE_BYTES = 512 << 20
+
+# Tiling of the headline configuration (tile rows, tile columns, states per
+# lane); see pick_tiling for the trade-off between parallelism and per-state
+# overhead.
+DEFAULT_TILING = (4, 2240, 1)
+
+
+def algorithmic_bytes(enc, rows, cols, batch=1):
+    """Bytes one GEMV must move: the whole compressed matrix (payload and
+    padding words, tile offsets, per-state offsets and initial states, the
+    16 KB table, the escape side table), x (bf16), the step vector (f32) and
+    y (f32)."""
+    comp = (enc["words"].nbytes + enc["tile_off"].nbytes + enc["soffs"].nbytes +
+            enc["states"].nbytes + enc["table"].nbytes + enc["esc_rowptr"].nbytes +
+            enc["esc_col"].nbytes + enc["esc_val"].nbytes)
+    return comp, comp + cols * 2 * batch + cols * 4 + rows * 4 * batch
+
+
+def graph_time_us(fns, steps, warmup):
+    """Device microseconds per call of K=steps calls captured in one graph."""
+    for i in range(warmup):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fns[0]()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fns[i % len(fns)]()
+    g.replay()  # untimed: first replay uploads the graph
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / steps
+
+
+def cpu_baseline(codes, step, x, budget_s=12.0):
+    """The oracle's scalar restatement of the reference decoder
+    (kernel/rans.py:101-123, one core: a pure-Python loop) on a bounded
+    sample of lanes of the reference 32-lane encoding (R=8, C=8960, the
+    published tiling for this shape), extrapolated to the whole matrix, plus
+    the numpy dense GEMV timed on the full matrix."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    from threadpoolctl import threadpool_info
+    enc = oracle.encode_ref(np.clip(codes, -128, 127), 8, COLS)
+    n = (COLS // 32) * 8
+    t0 = time.perf_counter()
+    oracle.decode_ref_py(enc, max_lanes=16)
+    per_lane = (time.perf_counter() - t0) / 16
+    lanes = int(max(16, min(len(enc["offs"]), budget_s / max(per_lane, 1e-9))))
+    t0 = time.perf_counter()
+    oracle.decode_ref_py(enc, max_lanes=lanes)
+    t_dec = time.perf_counter() - t0
+    per_sym = t_dec / (lanes * n)
+    t_decode_full = per_sym * codes.size
+    W = codes.astype(np.float32)
+    xs = x.astype(np.float32) * step
+    t0 = time.perf_counter()
+    for _ in range(5):
+        W @ xs
+    t_gemv = (time.perf_counter() - t0) / 5
+    t = t_decode_full + t_gemv
+    blas = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    return {"value": ROWS * COLS * 2 / t / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": (f"scalar decode of {lanes} of {len(enc['offs'])} lanes ({lanes * n} symbols, "
+                       f"{t_dec:.1f} s, {per_sym * 1e9:.0f} ns/symbol) extrapolated to "
+                       f"{codes.size} symbols = {t_decode_full:.1f} s, plus numpy dense GEMV "
+                       f"{t_gemv * 1e3:.1f} ms on {blas} BLAS threads"),
+            "us_per_gemv": t * 1e6, "host_cpus": len(os.sched_getaffinity(0)),
+            "numpy": np.__version__}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--tiling", type=str, default=None, help="R,C,S")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-rocblas", action="store_true")
+    ap.add_argument("--sweep", action="store_true", help="print a tiling sweep to stderr")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the matrix would shard by tile rows; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+
+    lib = rans.build()
+    codes = B.synth_codes_full(ROWS, COLS, BITS, seed=ROWS + COLS)
+    step = B.lognormal_steps(COLS, seed=ROWS + COLS)
+    x = np.random.default_rng(0).standard_normal(COLS).astype(np.float32)
+    xb = torch.from_numpy(x).cuda().bfloat16()
+    step_t = torch.from_numpy(step)
+    print(f"workload ready: entropy {B.entropy_fast(codes):.4f} bits", file=sys.stderr, flush=True)
+
+    def measure(R, C, S, steps):
+        enc = rans.encode(codes, R, C, S)
+        comp, alg = algorithmic_bytes(enc, ROWS, COLS)
+        ncopy = max(2, -(-ROTATE_BYTES // comp))
+        ms = [rans.RansMatrix(enc, step_t, lib) for _ in range(ncopy)]
+        y = torch.empty(ROWS, device="cuda")
+        fns = [lambda m=m: m.gemv(xb, y) for m in ms]
+        t_rot = graph_time_us(fns, steps, args.warmup)
+        t_hot = graph_time_us(fns[:1], steps, args.warmup)
+        del ms
+        torch.cuda.empty_cache()
+        return enc, comp, alg, ncopy, t_rot, t_hot
+
+    if args.sweep:
+        for S in (1, 2, 4):
+            for R in (1, 2, 4, 8, 16):
+                for C in (640, 1280, 1792, 2240, 4480, 8960):
+                    if C % (64 * S) or COLS % C:
+                        continue
+                    try:
+                        enc, comp, alg, ncopy, t_rot, t_hot = measure(R, C, S, 100)
+                    except AssertionError as e:
+                        print(f"sweep R={R} C={C} S={S}: {e}", file=sys.stderr)
+                        continue
+                    bt = 8 * comp / codes.size
+                    print(f"sweep R={R:2d} C={C:5d} S={S} states={len(enc['states']):7d} "
+                          f"bits_total={bt:.3f} rot={t_rot:7.2f}us hot={t_hot:7.2f}us "
+                          f"eff={ROWS * COLS * 2 / t_rot / 1e3:7.1f}GB/s", file=sys.stderr, flush=True)
+
+    R, C, S = (int(v) for v in args.tiling.split(",")) if args.tiling else DEFAULT_TILING
+    enc, comp, alg, ncopy, t_rot, t_hot = measure(R, C, S, args.steps)
+    bits_total = 8 * comp / codes.size
+    print(f"rans gemv: {t_rot:.2f} us rotated, {t_hot:.2f} us hot", file=sys.stderr, flush=True)
+
+    rocblas = None
+    if not args.no_rocblas:
+        W = (torch.from_numpy(codes.astype(np.float32)) * step_t).bfloat16()
+        nW = max(2, -(-ROTATE_BYTES // (ROWS * COLS * 2)))
+        Ws = [W.cuda() for _ in range(nW)]
+        fns = [lambda Wd=Wd: torch.nn.functional.linear(xb, Wd) for Wd in Ws]
+        tb_rot = graph_time_us(fns, args.steps, args.warmup)
+        tb_hot = graph_time_us(fns[:1], args.steps, args.warmup)
+        rocblas = {"us_per_gemv": tb_rot, "effective_GBps": ROWS * COLS * 2 / tb_rot / 1e3,
+                   "hot_us_per_gemv": tb_hot, "copies": nW,
+                   "speedup_rans_vs_bf16": tb_rot / t_rot}
+        del Ws
+        torch.cuda.empty_cache()
+        print(f"bf16 F.linear: {tb_rot:.2f} us rotated, {tb_hot:.2f} us hot", file=sys.stderr,
+              flush=True)
+
+    cpu = None if args.no_cpu else cpu_baseline(codes, step, torch.from_numpy(x).bfloat16().float().numpy())
+
+    achieved = alg / (t_rot * 1e-6) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": ROWS * COLS * 2 / t_rot / 1e3,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": t_rot / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32 decode / f32 accumulate",
+        "data": "synthetic",
+        "config": {"workload": f"{ROWS}x{COLS} Laplace ECSQ codes at {BITS} bits/weight entropy, "
+                               "log-normal per-column steps, bf16 x, batch 1",
+                   "rows": ROWS, "cols": COLS, "batch": 1, "R": R, "C": C, "S": S,
+                   "states": int(len(enc["states"])), "bits_total": bits_total,
+                   "bits_payload": enc["bits_payload"], "rotating_copies": ncopy,
+                   "parallelism": "single GPU"},
+        "us_per_gemv": t_rot,
+        "hot_us_per_gemv": t_hot,
+        "hot_effective_GBps": ROWS * COLS * 2 / t_hot / 1e3,
+        "compressed_GBps": comp / t_rot / 1e3,
+        "rocblas_bf16": rocblas,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "rans_w64_gemv_kernel", "bytes_per_launch": alg},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

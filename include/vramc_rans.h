@@ -1,0 +1,144 @@
+/*
+ * vramc_rans.h -- C ABI of librans_hip.so: entropy-coded (rANS) weight
+ * matrices decoded inside a batch-1 GEMV on MI355X (gfx950).
+ *
+ * Drop-in boundary for kernel/rans.py + kernel/rans_gemv.cu of
+ * snuri00/vram-compression.  The reference's C ABI (rans_gemv.cu:146-170)
+ * passes a flat list of raw pointers for its 32-lane stream; the wavefront
+ * stream format here carries more buffers (per-tile offsets, per-state
+ * initial states, an escape side table, the per-column step), so they travel
+ * in one plain-C descriptor, rans_w64_matrix, passed by pointer.  Every
+ * pointer in it is a device pointer owned by the caller (the Python wrapper
+ * keeps the tensors alive, as rans.py:134-137 does); the library keeps no
+ * state between calls except the per-process kernel attribute setup.
+ *
+ * Conventions kept from the reference:
+ *   - launches are asynchronous on the caller's stream (hipStream_t, e.g.
+ *     torch.cuda.current_stream().cuda_stream);
+ *   - the return value is 0 on success, a hipError_t value for a launch
+ *     error (hipGetLastError after the launch), or a negative value for a
+ *     rejected argument (the reference returns -1 for an unsupported R,
+ *     rans_gemv.cu:143).  No call synchronises.
+ *
+ * Stream format "w64" (all integers little endian):
+ *   - W (rows x cols) holds integer codes; W_real[r,c] = code[r,c]*step[c].
+ *   - The matrix is cut into tiles of R rows x C columns, tile t = rb*(cols/C)+cb.
+ *     A tile is decoded by one 64-lane wavefront with S rANS states per lane;
+ *     state j = s*64 + l decodes, for k < C/(64*S) and r < R (k-major,
+ *     r-minor), the code at row rb*R+r, column cb*C + 64*(S*k+s) + l.
+ *   - Coder arithmetic is the reference's (rans.py:13-16, rans_gemv.cu:32-37):
+ *     32-bit state, 16-bit renormalisation words, 12-bit probabilities,
+ *     table[slot] = sym | freq<<8 | (slot-cum)<<20, sym = code + 128.
+ *   - Symbol 0 is the escape: codes outside [-127, 127] are coded as symbol 0
+ *     and their values live in a CSR side table (esc_rowptr/esc_col/esc_val,
+ *     columns ascending within a row).
+ *   - words: all tile blocks concatenated; tile t's block is
+ *     words[tile_off[t] .. tile_off[t+1]), a multiple of 8 words with at least
+ *     one trailing pad word; state j's stream starts at tile_off[t]+soffs[t*64*S+j]
+ *     and lists its renormalisation words in decode order.  states[] holds
+ *     each state's initial (decoder) value.
+ */
+#ifndef VRAMC_RANS_H
+#define VRAMC_RANS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* x dtype codes for launch_rans_gemv */
+#define RANS_X_F32 0
+#define RANS_X_BF16 1
+
+/* rejected-argument return values */
+#define RANS_EUNSUPPORTED (-1) /* R, S or batch without a compiled kernel */
+#define RANS_EGEOMETRY (-2)    /* shape not divisible, or tile too large for LDS */
+#define RANS_EWORKSPACE (-3)   /* split-K workspace missing or too small */
+#define RANS_EARG (-4)         /* null pointer or negative size */
+#define RANS_ECODES (-5)       /* encoder: degenerate or empty symbol distribution */
+#define RANS_ETILE (-6)        /* encoder: a tile block exceeds 65535 words */
+
+typedef struct rans_w64_matrix {
+    int32_t rows, cols;       /* out_features, in_features */
+    int32_t R, C, S;          /* tile rows, tile columns, states per lane */
+    int32_t max_tile_words;   /* largest tile block, in 16-bit words */
+    const uint16_t* words;    /* [tile_off[ntiles]] */
+    const uint32_t* tile_off; /* [ntiles+1], in words, multiples of 8 */
+    const uint16_t* soffs;    /* [ntiles*64*S] */
+    const uint32_t* states;   /* [ntiles*64*S] */
+    const uint32_t* table;    /* [4096], reference packing */
+    const int32_t* esc_rowptr;/* [rows+1] */
+    const int32_t* esc_col;   /* [nesc] */
+    const int32_t* esc_val;   /* [nesc] */
+    const float* step;        /* [cols] per-column step (waterfilling) */
+    void* workspace;          /* split-K partials + counters; zero-filled once */
+    int64_t workspace_bytes;
+} rans_w64_matrix;
+
+/* ---------------------------------------------------------------- device */
+
+/* Fused decode + GEMV: y[b, r] = sum_c code[r,c] * (x[b,c] * step[c]) for
+ * b < batch.  x is batch x cols (f32 or bf16, RANS_X_*), y is batch x rows
+ * f32, written (never accumulated into).  The per-column step is folded into
+ * x inside the kernel.  Replaces launch_rans_gemv (rans_gemv.cu:146-153),
+ * which takes a host-folded f32 x and needs y zeroed when cols != C. */
+int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
+                     void* y, hipStream_t stream);
+
+/* Bytes of workspace launch_rans_gemv needs for this matrix and batch (0 when
+ * one workgroup covers a whole tile row).  The first 4096 bytes are counters
+ * that must be zero before the first launch; the kernel leaves them zero. */
+int64_t rans_gemv_workspace_bytes(const rans_w64_matrix* m, int batch);
+
+/* Decode to a dense bf16 matrix out[r,c] = bf16(code[r,c]*step[c]) (round to
+ * nearest even).  Replaces launch_rans_decode (rans_gemv.cu:155-162). */
+int launch_rans_decode(const rans_w64_matrix* m, void* out_bf16, hipStream_t stream);
+
+/* Decode to dense int32 codes out[r,c] = code[r,c], escapes included: the
+ * bit-exact check path.  No reference counterpart (the reference compares
+ * the bf16 decode, bench.py:49-51). */
+int launch_rans_decode_codes(const rans_w64_matrix* m, int32_t* out, hipStream_t stream);
+
+/* Fixed-rate 4-bit baseline GEMV, same contract as the reference
+ * (rans_gemv.cu:164-170): w packs 8 codes per u32 (nibble b of word j of row
+ * r is column 8j+b, value nibble-8), x is the host-folded f32 x*step, y f32. */
+int launch_int4_gemv(const void* w, const void* x, void* y, int rows, int cols,
+                     hipStream_t stream);
+
+/* ------------------------------------------------------------------ host */
+
+/* Static 12-bit table from a symbol histogram, rans.py:34-51: freq[256],
+ * cum[256], table[4096].  Returns RANS_ECODES for an empty or single-symbol
+ * distribution. */
+int rans_build_table(const uint8_t* sym, int64_t n, int64_t* freq, int64_t* cum,
+                     uint32_t* table);
+
+/* Encode int32 codes (rows x cols, row-major) into the w64 format; replaces
+ * encode() (rans.py:62-98).  On success *handle owns the result and info[]
+ * receives {nwords, ntiles, nstates, nesc, max_tile_words, payload_words}.
+ * Fetch the arrays with rans_w64_encode_fetch, then free the handle. */
+int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols, int32_t R, int32_t C,
+                    int32_t S, int32_t nthreads, void** handle, int64_t* info);
+
+int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off, uint16_t* soffs,
+                          uint32_t* states, uint32_t* table, int64_t* freq,
+                          int32_t* esc_rowptr, int32_t* esc_col, int32_t* esc_val);
+
+void rans_w64_encode_free(void* handle);
+
+/* Host decoder of the w64 format to int32 codes (escapes applied); replaces
+ * decode_ref (rans.py:101-123).  Returns state+1 (positive) for the first
+ * state whose final value is not 2^16 (the reference's final-state assert,
+ * rans.py:121), RANS_EARG on a stream overrun or an escape side table that
+ * disagrees with the escape symbols in the stream. */
+int rans_w64_decode_host(const rans_w64_matrix* m_host, int32_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VRAMC_RANS_H */

@@ -1,0 +1,83 @@
+"""The C-ABI library loads on a machine without a GPU, exports every entry
+point include/vramc_rans.h declares, and rejects bad arguments before any
+HIP call (no compute happens in these tests)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vramc_rans.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^(?:int|int64_t|void)\s+(\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "launch_rans_gemv" in names and "launch_int4_gemv" in names
+    assert len(names) == len(set(names))
+
+
+def test_every_declared_symbol_is_exported(rans, lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert set(_declared()) == set(rans.EXPORTS)
+
+
+def _desc(rans, rows=256, cols=4096, R=8, C=256, S=1, mtw=1024):
+    fake = 0x1000  # never dereferenced: every call below returns before launching
+    return rans.RansMatrixDesc(rows=rows, cols=cols, R=R, C=C, S=S, max_tile_words=mtw,
+                               words=fake, tile_off=fake, soffs=fake, states=fake, table=fake,
+                               esc_rowptr=fake, esc_col=fake, esc_val=fake, step=fake,
+                               workspace=None, workspace_bytes=0)
+
+
+def test_argument_validation_without_gpu(rans, lib):
+    d = _desc(rans)
+    x = y = ctypes.c_void_p(0x2000)
+    assert lib.launch_rans_gemv(None, x, 0, 1, y, None) == -2
+    bad = _desc(rans, cols=4000)
+    assert lib.launch_rans_gemv(ctypes.byref(bad), x, 0, 1, y, None) == -2
+    r3 = _desc(rans, rows=255, R=3)
+    assert lib.launch_rans_gemv(ctypes.byref(r3), x, 0, 1, y, None) == -1
+    assert lib.launch_rans_gemv(ctypes.byref(d), x, 7, 1, y, None) == -4
+    assert lib.launch_rans_gemv(ctypes.byref(d), None, 0, 1, y, None) == -4
+    assert lib.launch_rans_gemv(ctypes.byref(d), x, 0, 0, y, None) == -4
+    # 16 column tiles: 8 waves per workgroup, 2 column groups -> split-K workspace
+    assert lib.launch_rans_gemv(ctypes.byref(d), x, 0, 1, y, None) == -3
+    need = lib.rans_gemv_workspace_bytes(ctypes.byref(d), 1)
+    assert need == 256 + 2 * 1 * 256 * 4
+    assert lib.rans_gemv_workspace_bytes(ctypes.byref(d), 4) == 256 + 2 * 4 * 256 * 4
+    one = _desc(rans, cols=2048)  # 8 column tiles: one workgroup per tile row
+    assert lib.rans_gemv_workspace_bytes(ctypes.byref(one), 1) == 0
+    huge = _desc(rans, mtw=70000)
+    assert lib.rans_gemv_workspace_bytes(ctypes.byref(huge), 1) == -2
+    assert lib.launch_rans_decode(None, y, None) == -2
+    assert lib.launch_rans_decode_codes(ctypes.byref(d), None, None) == -4
+    assert lib.launch_int4_gemv(None, x, y, 4, 64, None) == -4
+    assert lib.launch_int4_gemv(x, x, y, 4, 48, None) == -2
+
+
+def test_product_fails_loudly_without_gpu(rans):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    import numpy as np
+    codes = np.random.default_rng(0).integers(-3, 4, size=(8, 64)).astype(np.int32)
+    enc = rans.encode(codes, 1, 64)
+    with pytest.raises(RuntimeError):
+        rans.RansMatrix(enc, np.ones(64, np.float32), rans._LIB)
+
+
+def test_oracle_is_not_imported_by_the_product():
+    pkg = os.path.join(ROOT, "vram-compression_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".cpp", ".h")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "import oracle" not in text and "liboracle" not in text, f

@@ -1,0 +1,177 @@
+"""Host side of the product (librans_hip.so's C++ encoder/decoder and the
+Python wrapper) checked against the oracle on the CPU."""
+import ctypes
+
+import numpy as np
+import pytest
+
+SHAPES = [  # rows, cols, R, C, S, bits
+    (64, 256, 4, 256, 1, 3.0),
+    (128, 512, 8, 128, 1, 2.0),
+    (256, 1024, 16, 512, 2, 4.0),
+    (32, 64, 1, 64, 1, 1.0),
+    (64, 512, 2, 256, 4, 3.0),
+    (48, 768, 16, 384, 2, 5.0),
+    (96, 1280, 8, 640, 1, 2.25),
+]
+
+
+def _ids(s):
+    return "x".join(str(v) for v in s)
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+def test_round_trip_matches_oracle(rans, oracle, shape):
+    rows, cols, R, C, S, bits = shape
+    codes = oracle.synth_codes(rows, cols, bits, seed=rows + cols)
+    enc = rans.encode(codes, R, C, S)
+    np.testing.assert_array_equal(rans.decode_ref(enc), codes)
+    np.testing.assert_array_equal(oracle.w64_decode(enc), codes)
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+def test_streams_equal_reference_encoder(rans, oracle, shape):
+    """Each w64 state's stream is exactly what the reference encoder
+    (kernel/rans.py:62-98, restated in the oracle) emits for that state's
+    symbol sequence: same table, same initial state, same words."""
+    rows, cols, R, C, S, bits = shape
+    codes = oracle.synth_codes(rows, cols, bits, seed=rows + cols + 1)
+    enc = rans.encode(codes, R, C, S)
+    sym = (codes + 128).astype(np.uint8)
+    freq, cum, table = oracle.build_table(sym)
+    np.testing.assert_array_equal(enc["table"], table)
+    seqs = np.ascontiguousarray(oracle.w64_order(sym, R, C, S))
+    lanes, n = seqs.shape
+    lib = oracle.load()
+    cap = lanes * (n + 2) + 8
+    words = np.zeros(cap, np.uint16)
+    offs = np.zeros(lanes, np.uint32)
+    counts = np.zeros(lanes, np.int64)
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    assert lib.orc_encode_lanes(p(seqs), lanes, n, p(freq), p(cum), p(words), cap, p(offs)) == 0
+    assert lib.orc_count_words(p(seqs), lanes, n, p(freq), p(cum), p(counts)) == 0
+    nst = 64 * S
+    for j in range(lanes):
+        o = int(offs[j])
+        assert int(enc["states"][j]) == (int(words[o]) << 16) | int(words[o + 1])
+        ref_words = words[o + 2:o + 2 + counts[j]]
+        t = j // nst
+        start = int(enc["tile_off"][t]) + int(enc["soffs"][j])
+        np.testing.assert_array_equal(enc["words"][start:start + counts[j]], ref_words)
+
+
+def test_escapes_round_trip(rans, oracle):
+    rng = np.random.default_rng(0)
+    codes = oracle.synth_codes(128, 256, 2.0, seed=1)
+    m = rng.random(codes.shape) < 0.01
+    codes[m] = rng.integers(128, 600, m.sum()) * rng.choice([-1, 1], m.sum())
+    codes[0, 0] = -128  # the reference alphabet's lowest code is an escape here
+    codes[5, 7] = 2 ** 30
+    codes[6, 8] = -(2 ** 31)
+    enc = rans.encode(codes, 4, 128, 1)
+    assert len(enc["esc_col"]) == int(((codes < -127) | (codes > 127)).sum())
+    np.testing.assert_array_equal(rans.decode_ref(enc), codes)
+    np.testing.assert_array_equal(oracle.w64_decode(enc), codes)
+    # side table is CSR by row with ascending columns
+    rp = enc["esc_rowptr"]
+    for r in range(codes.shape[0]):
+        cols = enc["esc_col"][rp[r]:rp[r + 1]]
+        assert np.all(np.diff(cols) > 0)
+
+
+def test_escape_side_table_must_match_stream(rans, oracle):
+    codes = oracle.synth_codes(64, 256, 3.0, seed=3)
+    codes[3, 4] = 500
+    enc = rans.encode(codes, 4, 256, 1)
+    bad = dict(enc)
+    bad["esc_col"] = enc["esc_col"] + 1
+    with pytest.raises(AssertionError):
+        rans.decode_ref(bad)
+    with pytest.raises(AssertionError):
+        oracle.w64_decode(bad)
+
+
+def test_corrupt_state_detected(rans, oracle):
+    codes = oracle.synth_codes(64, 256, 3.0, seed=4)
+    enc = rans.encode(codes, 4, 256, 1)
+    bad = dict(enc)
+    bad["states"] = enc["states"].copy()
+    bad["states"][0] ^= 0x5A5A
+    with pytest.raises(AssertionError):
+        rans.decode_ref(bad)
+    with pytest.raises(AssertionError):
+        oracle.w64_decode(bad)
+
+
+def test_encode_rejects_bad_input(rans):
+    ok = np.random.default_rng(0).integers(-3, 4, size=(16, 128)).astype(np.int32)
+    with pytest.raises(AssertionError):
+        rans.encode(np.full((16, 128), 5, np.int32), 4, 128)  # single symbol
+    with pytest.raises(AssertionError):
+        rans.encode(ok, 3, 128)  # rows % R
+    with pytest.raises(AssertionError):
+        rans.encode(ok, 4, 96)  # C % 64
+    with pytest.raises(AssertionError):
+        rans.encode(ok, 4, 128, S=4)  # C % (64*S)
+    with pytest.raises(AssertionError):
+        rans.encode(np.zeros((0, 128), np.int32), 1, 128)
+    # a tile block beyond 65535 words
+    big = np.random.default_rng(1).integers(-127, 128, size=(16, 65536)).astype(np.int32)
+    with pytest.raises(AssertionError):
+        rans.encode(big, 16, 65536)
+
+
+def test_build_table_matches_oracle(rans, oracle, golden):
+    for name in ["two_symbols", "tie_argmax", "rare_overflow", "half_even", "laplace"]:
+        sym = golden[f"tab_{name}_sym"]
+        for a, b in zip(rans.build_table(sym), oracle.build_table(sym)):
+            np.testing.assert_array_equal(a, b)
+
+
+def test_lane_order_matches_oracle(rans, oracle):
+    a = np.arange(32 * 1024).reshape(32, 1024)
+    for R, C, S in [(1, 64, 1), (4, 256, 2), (8, 1024, 4), (32, 512, 1)]:
+        np.testing.assert_array_equal(rans.lane_order(a, R, C, S), oracle.w64_order(a, R, C, S))
+
+
+def test_bit_accounting(rans, oracle):
+    rows, cols, R, C, S = 256, 1024, 8, 512, 1
+    codes = oracle.synth_codes(rows, cols, 3.0, seed=9)
+    enc = rans.encode(codes, R, C, S)
+    N = rows * cols
+    sym = (codes + 128).astype(np.uint8)
+    seqs = oracle.w64_order(sym, R, C, S)
+    freq, cum, _ = oracle.build_table(sym)
+    lib = oracle.load()
+    counts = np.zeros(seqs.shape[0], np.int64)
+    s = np.ascontiguousarray(seqs)
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    assert lib.orc_count_words(p(s), s.shape[0], s.shape[1], p(freq), p(cum), p(counts)) == 0
+    assert enc["bits_payload"] == 16 * counts.sum() / N
+    nstates = seqs.shape[0]
+    ntiles = (rows // R) * (cols // C)
+    pad = len(enc["words"]) - counts.sum()
+    assert enc["bits_state_offs"] == (48 * nstates + 32 * (ntiles + 1) + 16 * pad) / N
+    assert enc["bits_table"] == 32 * 4096 / N
+    assert 0 < pad <= 8 * ntiles
+    assert np.all(np.diff(enc["tile_off"].astype(np.int64)) % 8 == 0)
+
+
+def test_bench_generators(rans, oracle, golden):
+    import rans_bench as B
+    for i in range(4):
+        rows, cols, R, C = (int(v) for v in golden[f"enc{i}_meta"])
+        bits = float(golden[f"enc{i}_bits"][0])
+        np.testing.assert_array_equal(B.synth_codes(rows, cols, bits, seed=rows),
+                                      golden[f"enc{i}_codes"])
+    c = B.synth_codes_full(512, 1024, 3.25, seed=5)
+    assert abs(B.entropy(c) - 3.25) <= 0.005
+    assert B.entropy_fast(c) == pytest.approx(B.entropy(c), abs=1e-12)
+    c = B.synth_codes_full(256, 1024, 2.25, dist="student3", seed=6, escape_frac=0.01)
+    assert abs(int(((c < -127) | (c > 127)).sum()) - 0.01 * c.size) <= 0.002 * c.size
+    st = B.lognormal_steps(1024, seed=1)
+    assert st.shape == (1024,) and np.all(st > 0)
+    for rows, cols in [(1536, 8960), (8960, 1536), (256, 1536), (25600, 5120)]:
+        for S in (1, 2):
+            R, C = B.pick_tiling(rows, cols, S=S)
+            assert rows % R == 0 and cols % C == 0 and C % (64 * S) == 0

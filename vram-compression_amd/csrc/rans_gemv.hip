@@ -1,0 +1,610 @@
+// Fused rANS decode + batch-1 GEMV for entropy-coded weight codes, written
+// for MI355X (gfx950, CDNA4, wave64).  The stream format is the "w64" layout
+// documented in include/vramc_rans.h.
+//
+// Kernel shape (one workgroup = W wavefronts = W tiles of one tile row):
+//   1. the 4096-slot symbol table is expanded into LDS as {freq | code<<24,
+//      slot-cum} pairs, so one ds_read_b64 yields both rANS operands and the
+//      signed code (the reference keeps sym|freq<<8|bias<<20 and extracts the
+//      fields with three more ALU ops per symbol, rans_gemv.cu:33-36);
+//   2. each wavefront copies its tile's whole compressed block into its own
+//      LDS region with 16-byte loads (coalesced across the 64 lanes), so the
+//      data-dependent renormalisation reads hit LDS, not HBM;
+//   3. each lane runs S independent rANS states; per column step k a lane
+//      loads x[c]*step[c] once (the waterfilling fold happens here) and
+//      reuses it for the R rows of the tile;
+//   4. row sums are reduced across the 64 lanes with cross-lane shuffles and
+//      across the W waves through LDS in a fixed order, escapes are added
+//      from the CSR side table, and y is written; when one workgroup does not
+//      cover all column tiles, partial sums go to a workspace and the last
+//      workgroup of the tile row adds them up in a fixed order (no atomics on
+//      y, no memset, deterministic).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+
+#include "../../include/vramc_rans.h"
+
+namespace {
+
+constexpr uint32_t kProbM = 4096;
+constexpr uint32_t kRansL = 1u << 16;
+constexpr int kMaxWaves = 8;
+constexpr int kMaxRB = 64;  // largest R*B compiled (16 * 4)
+
+// LDS layout of the GEMV/decode kernels (bytes).
+constexpr int kTabOff = 0;                          // uint2[4096]
+constexpr int kRedOff = kTabOff + 8 * (int)kProbM;  // float[kMaxWaves*kMaxRB]
+constexpr int kEscOff = kRedOff + 4 * kMaxWaves * kMaxRB;  // float[kMaxRB]
+constexpr int kFlagOff = kEscOff + 4 * kMaxRB;      // int
+constexpr int kTileOff = kFlagOff + 16;             // per-wave tile regions
+constexpr int kLdsMax = 160 * 1024;
+
+static_assert(kTileOff % 16 == 0, "tile regions must be 16-byte aligned");
+
+struct GemvArgs {
+    const uint16_t* words;
+    const uint32_t* tile_off;
+    const uint16_t* soffs;
+    const uint32_t* states;
+    const uint32_t* table;
+    const int32_t* esc_rowptr;
+    const int32_t* esc_col;
+    const int32_t* esc_val;
+    const float* step;
+    const void* x;
+    float* y;
+    float* partial;      // [ngroups][B][rows]
+    uint32_t* counters;  // [rows/R]
+    int rows, cols, C, ncb, ngroups, tile_lds_words;
+};
+
+struct DecodeArgs {
+    const uint16_t* words;
+    const uint32_t* tile_off;
+    const uint16_t* soffs;
+    const uint32_t* states;
+    const uint32_t* table;
+    const float* step;
+    void* out;
+    int rows, cols, C, ncb, ntiles, tile_lds_words;
+};
+
+// Expands the reference-packed table (sym | freq<<8 | bias<<20) into LDS
+// pairs {freq | code<<24, bias}; the escape symbol (0) gets code 0 so it adds
+// nothing in the GEMV and is patched from the side table afterwards.
+__device__ inline void stage_table(uint2* tab, const uint32_t* __restrict__ table) {
+    for (int i = threadIdx.x; i < (int)kProbM; i += blockDim.x) {
+        const uint32_t e = table[i];
+        const uint32_t sym = e & 0xFFu;
+        const uint32_t code = sym == 0 ? 0u : (uint32_t)((int32_t)sym - 128);
+        tab[i] = make_uint2(((e >> 8) & 0xFFFu) | (code << 24), e >> 20);
+    }
+}
+
+// Copies tile t's compressed block (a multiple of 8 words) into this wave's
+// LDS region with 16-byte loads; never writes past max_words.
+__device__ inline void stage_tile(uint16_t* tw, const uint16_t* __restrict__ words,
+                                  const uint32_t* __restrict__ tile_off, int t, int lane,
+                                  int max_words) {
+    const uint32_t o0 = tile_off[t];
+    uint32_t nw = tile_off[t + 1] - o0;
+    if (nw > (uint32_t)max_words) nw = (uint32_t)max_words;
+    const uint4* src = reinterpret_cast<const uint4*>(words + o0);
+    uint4* dst = reinterpret_cast<uint4*>(tw);
+    for (uint32_t i = lane; i < (nw >> 3); i += 64) dst[i] = src[i];
+}
+
+__device__ inline float load_x(const void* x, int64_t i, bool bf16) {
+    if (bf16) {
+        const uint32_t v = reinterpret_cast<const uint16_t*>(x)[i];
+        return __uint_as_float(v << 16);
+    }
+    return reinterpret_cast<const float*>(x)[i];
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// One rANS decode step with the reference arithmetic (rans_gemv.cu:32-37):
+// e = tab[st & 4095]; st = freq*(st>>12) + bias; renormalise from the LDS
+// word stream when st < 2^16.  w holds the next unread word of the stream
+// (prefetched), p its index in the wave's LDS region.
+__device__ inline int32_t rans_step(uint32_t& st, uint32_t& p, uint32_t& w, const uint2* tab,
+                                    const uint16_t* tw) {
+    const uint2 e = tab[st & (kProbM - 1)];
+    const uint32_t ns = __umul24(e.x, st >> 12) + e.y;  // freq < 2^12, st>>12 < 2^20
+    const bool need = ns < kRansL;
+    const uint32_t rn = (ns << 16) | w;
+    st = need ? rn : ns;
+    p += need ? 1u : 0u;
+    w = tw[p];
+    return (int32_t)e.x >> 24;
+}
+
+template <int R, int S, int B, bool XBF16>
+__global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint2* tab = reinterpret_cast<uint2*>(lds + kTabOff);
+    float* red = reinterpret_cast<float*>(lds + kRedOff);
+    float* esc_red = reinterpret_cast<float*>(lds + kEscOff);
+    int* flag = reinterpret_cast<int*>(lds + kFlagOff);
+    const int W = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    uint16_t* tw = reinterpret_cast<uint16_t*>(lds + kTileOff) + (size_t)wave * a.tile_lds_words;
+
+    const int rb = blockIdx.x / a.ngroups;
+    const int g = blockIdx.x - rb * a.ngroups;
+    const int cb = g * W + wave;
+    const bool active = cb < a.ncb;
+    const int t = rb * a.ncb + cb;
+
+    stage_table(tab, a.table);
+    if (active) stage_tile(tw, a.words, a.tile_off, t, lane, a.tile_lds_words);
+    if (threadIdx.x < R * B) esc_red[threadIdx.x] = 0.f;
+    __syncthreads();
+
+    float acc[R][B];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < B; b++) acc[r][b] = 0.f;
+
+    if (active) {
+        uint32_t st[S], p[S], w[S];
+        const int sbase = t * 64 * S + lane;
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            st[s] = a.states[sbase + 64 * s];
+            p[s] = a.soffs[sbase + 64 * s];
+        }
+#pragma unroll
+        for (int s = 0; s < S; s++) w[s] = tw[p[s]];
+        const int nk = a.C / (64 * S);
+        const int colbase = cb * a.C + lane;
+        for (int k = 0; k < nk; k++) {
+            float xv[S][B];
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                const int col = colbase + 64 * (S * k + s);
+                const float sc = a.step[col];
+#pragma unroll
+                for (int b = 0; b < B; b++)
+                    xv[s][b] = load_x(a.x, (int64_t)b * a.cols + col, XBF16) * sc;
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+#pragma unroll
+                for (int s = 0; s < S; s++) {
+                    const float code = (float)rans_step(st[s], p[s], w[s], tab, tw);
+#pragma unroll
+                    for (int b = 0; b < B; b++) acc[r][b] = fmaf(code, xv[s][b], acc[r][b]);
+                }
+            }
+        }
+    }
+
+    // Escapes of this tile row (added once, by column group 0): wave w takes
+    // rows r = w, w+W, ..., its lanes stride over the row's side-table entries.
+    if (g == 0) {
+        for (int r = wave; r < R; r += W) {
+            const int row = rb * R + r;
+            const int e0 = a.esc_rowptr[row], e1 = a.esc_rowptr[row + 1];
+            if (e0 == e1) continue;
+            float es[B];
+#pragma unroll
+            for (int b = 0; b < B; b++) es[b] = 0.f;
+            for (int e = e0 + lane; e < e1; e += 64) {
+                const int col = a.esc_col[e];
+                const float v = (float)a.esc_val[e] * a.step[col];
+#pragma unroll
+                for (int b = 0; b < B; b++)
+                    es[b] = fmaf(v, load_x(a.x, (int64_t)b * a.cols + col, XBF16), es[b]);
+            }
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const float v = wave_sum(es[b]);
+                if (lane == 0) esc_red[r * B + b] = v;
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const float v = wave_sum(acc[r][b]);
+            if (lane == 0) red[wave * (R * B) + r * B + b] = v;
+        }
+    }
+    __syncthreads();
+
+    const int tid = threadIdx.x;
+    float v = 0.f;
+    int row = 0, b = 0;
+    if (tid < R * B) {
+        const int r = tid / B;
+        b = tid - r * B;
+        row = rb * R + r;
+        for (int ww = 0; ww < W; ww++) v += red[ww * (R * B) + tid];
+        v += esc_red[tid];
+    }
+    if (a.ngroups == 1) {
+        if (tid < R * B) a.y[(int64_t)b * a.rows + row] = v;
+        return;
+    }
+
+    // Split over column groups: publish the partial, count arrivals, and let
+    // the last workgroup of this tile row sum the partials in group order.
+    if (tid < R * B)
+        __hip_atomic_store(&a.partial[((int64_t)g * B + b) * a.rows + row], v, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(&a.counters[rb], 1u, __ATOMIC_ACQ_REL,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old == (uint32_t)(a.ngroups - 1);
+    }
+    __syncthreads();
+    if (*flag) {
+        __threadfence();
+        if (tid < R * B) {
+            float s = 0.f;
+            for (int gg = 0; gg < a.ngroups; gg++)
+                s += __hip_atomic_load(&a.partial[((int64_t)gg * B + b) * a.rows + row],
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            a.y[(int64_t)b * a.rows + row] = s;
+        }
+        if (tid == 0)
+            __hip_atomic_store(&a.counters[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+__device__ inline uint16_t f32_to_bf16_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu))  // NaN stays NaN
+        return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Decode only.  MODE 0 writes int32 codes, MODE 1 writes bf16(code*step[c]).
+// One wave per tile; escapes are written afterwards by scatter_escapes.
+template <int R, int S, int MODE>
+__global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint2* tab = reinterpret_cast<uint2*>(lds + kTabOff);
+    const int W = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    uint16_t* tw = reinterpret_cast<uint16_t*>(lds + kTileOff) + (size_t)wave * a.tile_lds_words;
+    const int t = blockIdx.x * W + wave;
+    const bool active = t < a.ntiles;
+
+    stage_table(tab, a.table);
+    if (active) stage_tile(tw, a.words, a.tile_off, t, lane, a.tile_lds_words);
+    __syncthreads();
+    if (!active) return;
+
+    const int rb = t / a.ncb, cb = t - rb * a.ncb;
+    uint32_t st[S], p[S], w[S];
+    const int sbase = t * 64 * S + lane;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        st[s] = a.states[sbase + 64 * s];
+        p[s] = a.soffs[sbase + 64 * s];
+    }
+#pragma unroll
+    for (int s = 0; s < S; s++) w[s] = tw[p[s]];
+    const int nk = a.C / (64 * S);
+    const int colbase = cb * a.C + lane;
+    for (int k = 0; k < nk; k++) {
+        // Symbol order within a state is k-major, r-minor; the S states of a
+        // lane advance together per row, as in the GEMV.
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                const int col = colbase + 64 * (S * k + s);
+                const int32_t code = rans_step(st[s], p[s], w[s], tab, tw);
+                const int64_t o = ((int64_t)rb * R + r) * a.cols + col;
+                if (MODE == 0)
+                    reinterpret_cast<int32_t*>(a.out)[o] = code;
+                else
+                    reinterpret_cast<uint16_t*>(a.out)[o] =
+                        f32_to_bf16_rne((float)code * a.step[col]);
+            }
+        }
+    }
+}
+
+template <int MODE>
+__global__ void scatter_escapes_kernel(const int32_t* __restrict__ rowptr,
+                                       const int32_t* __restrict__ ecol,
+                                       const int32_t* __restrict__ eval,
+                                       const float* __restrict__ step, void* out, int rows,
+                                       int cols) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    for (int e = rowptr[row]; e < rowptr[row + 1]; e++) {
+        const int col = ecol[e];
+        const int64_t o = (int64_t)row * cols + col;
+        if (MODE == 0)
+            reinterpret_cast<int32_t*>(out)[o] = eval[e];
+        else
+            reinterpret_cast<uint16_t*>(out)[o] = f32_to_bf16_rne((float)eval[e] * step[col]);
+    }
+}
+
+// Fixed-rate 4-bit baseline, the reference's contract (rans_gemv.cu:107-131):
+// one wavefront per row, each lane reads 16 bytes (32 codes) per step.
+__global__ void __launch_bounds__(256) int4_gemv_kernel(const uint32_t* __restrict__ w,
+                                                        const float* __restrict__ x,
+                                                        float* __restrict__ y, int rows,
+                                                        int cols) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint4* wr = reinterpret_cast<const uint4*>(w + (int64_t)row * (cols / 8));
+    float acc = 0.f;
+    for (int j = lane; j < cols / 32; j += 64) {
+        const uint4 q = wr[j];
+        const uint32_t qs[4] = {q.x, q.y, q.z, q.w};
+        const float4* xp = reinterpret_cast<const float4*>(x + j * 32);
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const float4 x0 = xp[2 * a], x1 = xp[2 * a + 1];
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int b = 0; b < 8; b++)
+                acc = fmaf((float)((int)((qs[a] >> (4 * b)) & 15u) - 8), xs[b], acc);
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+}
+
+// ------------------------------------------------------------------ host
+int tile_lds_words(const rans_w64_matrix* m) { return (m->max_tile_words + 7) & ~7; }
+
+size_t lds_bytes(int waves, int tw_words) { return (size_t)kTileOff + (size_t)waves * tw_words * 2; }
+
+bool valid_geometry(const rans_w64_matrix* m) {
+    if (!m || m->rows <= 0 || m->cols <= 0 || m->R <= 0 || m->C <= 0 || m->S <= 0) return false;
+    if (m->rows % m->R || m->cols % m->C || m->C % (64 * m->S)) return false;
+    if (m->max_tile_words <= 0 || m->max_tile_words > 65536) return false;
+    return true;
+}
+
+bool valid_pointers(const rans_w64_matrix* m) {
+    return m->words && m->tile_off && m->soffs && m->states && m->table && m->step &&
+           m->esc_rowptr && m->esc_col && m->esc_val;
+}
+
+// Waves per GEMV workgroup: the largest divisor of ncb up to kMaxWaves whose
+// LDS footprint fits.  Returns 0 when even one wave does not fit.
+int gemv_waves(const rans_w64_matrix* m) {
+    const int ncb = m->cols / m->C;
+    const int tw = tile_lds_words(m);
+    for (int w = kMaxWaves; w >= 1; w--)
+        if (ncb % w == 0 && lds_bytes(w, tw) <= (size_t)kLdsMax) return w;
+    return 0;
+}
+
+int decode_waves(const rans_w64_matrix* m) {
+    const int tw = tile_lds_words(m);
+    for (int w = 4; w >= 1; w >>= 1)
+        if (lds_bytes(w, tw) <= (size_t)kLdsMax) return w;
+    return 0;
+}
+
+size_t counters_bytes(const rans_w64_matrix* m) {
+    return (((size_t)(m->rows / m->R) * 4 + 255) / 256) * 256;
+}
+
+// Opt in to more than 64 KB of dynamic LDS once per kernel.
+std::mutex g_attr_mu;
+const void* g_attr_done[512];
+int g_attr_n = 0;
+
+hipError_t ensure_lds(const void* fn, size_t bytes) {
+    if (bytes <= 65536) return hipSuccess;
+    std::lock_guard<std::mutex> lk(g_attr_mu);
+    for (int i = 0; i < g_attr_n; i++)
+        if (g_attr_done[i] == fn) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+    if (e == hipSuccess && g_attr_n < 512) g_attr_done[g_attr_n++] = fn;
+    return e;
+}
+
+template <int R, int S, int B, bool XBF16>
+int launch_gemv_t(const GemvArgs& a, int waves, size_t lds, int grid, hipStream_t stream) {
+    const void* fn = reinterpret_cast<const void*>(&rans_w64_gemv_kernel<R, S, B, XBF16>);
+    hipError_t e = ensure_lds(fn, lds);
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL((rans_w64_gemv_kernel<R, S, B, XBF16>), dim3(grid), dim3(64 * waves), lds,
+                       stream, a);
+    return (int)hipGetLastError();
+}
+
+template <int R, int S, int B>
+int dispatch_x(const GemvArgs& a, bool xbf16, int waves, size_t lds, int grid, hipStream_t st) {
+    return xbf16 ? launch_gemv_t<R, S, B, true>(a, waves, lds, grid, st)
+                 : launch_gemv_t<R, S, B, false>(a, waves, lds, grid, st);
+}
+
+template <int R, int S>
+int dispatch_b(const GemvArgs& a, int B, bool xbf16, int waves, size_t lds, int grid,
+               hipStream_t st) {
+    switch (B) {
+        case 1: return dispatch_x<R, S, 1>(a, xbf16, waves, lds, grid, st);
+        case 4: return dispatch_x<R, S, 4>(a, xbf16, waves, lds, grid, st);
+        default: return RANS_EUNSUPPORTED;
+    }
+}
+
+template <int R>
+int dispatch_s(const GemvArgs& a, int S, int B, bool xbf16, int waves, size_t lds, int grid,
+               hipStream_t st) {
+    switch (S) {
+        case 1: return dispatch_b<R, 1>(a, B, xbf16, waves, lds, grid, st);
+        case 2: return dispatch_b<R, 2>(a, B, xbf16, waves, lds, grid, st);
+        case 4: return dispatch_b<R, 4>(a, B, xbf16, waves, lds, grid, st);
+        default: return RANS_EUNSUPPORTED;
+    }
+}
+
+int dispatch_gemv(const GemvArgs& a, int R, int S, int B, bool xbf16, int waves, size_t lds,
+                  int grid, hipStream_t st) {
+    switch (R) {
+        case 1: return dispatch_s<1>(a, S, B, xbf16, waves, lds, grid, st);
+        case 2: return dispatch_s<2>(a, S, B, xbf16, waves, lds, grid, st);
+        case 4: return dispatch_s<4>(a, S, B, xbf16, waves, lds, grid, st);
+        case 8: return dispatch_s<8>(a, S, B, xbf16, waves, lds, grid, st);
+        case 16: return dispatch_s<16>(a, S, B, xbf16, waves, lds, grid, st);
+        default: return RANS_EUNSUPPORTED;
+    }
+}
+
+bool supported_rs(int R, int S) {
+    return (R == 1 || R == 2 || R == 4 || R == 8 || R == 16) && (S == 1 || S == 2 || S == 4);
+}
+
+template <int R, int S, int MODE>
+int launch_decode_t(const DecodeArgs& a, int waves, size_t lds, int grid, hipStream_t stream) {
+    const void* fn = reinterpret_cast<const void*>(&rans_w64_decode_kernel<R, S, MODE>);
+    hipError_t e = ensure_lds(fn, lds);
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL((rans_w64_decode_kernel<R, S, MODE>), dim3(grid), dim3(64 * waves), lds,
+                       stream, a);
+    return (int)hipGetLastError();
+}
+
+template <int MODE>
+int dispatch_decode(const DecodeArgs& a, int R, int S, int waves, size_t lds, int grid,
+                    hipStream_t st) {
+#define VRAMC_DEC_CASE(RR, SS) \
+    if (R == RR && S == SS) return launch_decode_t<RR, SS, MODE>(a, waves, lds, grid, st);
+#define VRAMC_DEC_R(RR) VRAMC_DEC_CASE(RR, 1) VRAMC_DEC_CASE(RR, 2) VRAMC_DEC_CASE(RR, 4)
+    VRAMC_DEC_R(1) VRAMC_DEC_R(2) VRAMC_DEC_R(4) VRAMC_DEC_R(8) VRAMC_DEC_R(16)
+#undef VRAMC_DEC_R
+#undef VRAMC_DEC_CASE
+    return RANS_EUNSUPPORTED;
+}
+
+template <int MODE>
+int launch_decode_common(const rans_w64_matrix* m, void* out, hipStream_t stream) {
+    if (!valid_geometry(m)) return RANS_EGEOMETRY;
+    if (!valid_pointers(m) || !out) return RANS_EARG;
+    if (!supported_rs(m->R, m->S)) return RANS_EUNSUPPORTED;
+    const int waves = decode_waves(m);
+    if (!waves) return RANS_EGEOMETRY;
+    DecodeArgs a;
+    a.words = m->words;
+    a.tile_off = m->tile_off;
+    a.soffs = m->soffs;
+    a.states = m->states;
+    a.table = m->table;
+    a.step = m->step;
+    a.out = out;
+    a.rows = m->rows;
+    a.cols = m->cols;
+    a.C = m->C;
+    a.ncb = m->cols / m->C;
+    a.ntiles = (m->rows / m->R) * a.ncb;
+    a.tile_lds_words = tile_lds_words(m);
+    const int grid = (a.ntiles + waves - 1) / waves;
+    int rc = dispatch_decode<MODE>(a, m->R, m->S, waves, lds_bytes(waves, a.tile_lds_words), grid,
+                                   stream);
+    if (rc != 0) return rc;
+    hipLaunchKernelGGL((scatter_escapes_kernel<MODE>), dim3((m->rows + 255) / 256), dim3(256), 0,
+                       stream, m->esc_rowptr, m->esc_col, m->esc_val, m->step, out, m->rows,
+                       m->cols);
+    return (int)hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int64_t rans_gemv_workspace_bytes(const rans_w64_matrix* m, int batch) {
+    if (!valid_geometry(m) || batch <= 0) return RANS_EGEOMETRY;
+    const int waves = gemv_waves(m);
+    if (!waves) return RANS_EGEOMETRY;
+    const int ngroups = (m->cols / m->C) / waves;
+    if (ngroups <= 1) return 0;
+    const int bmax = batch >= 4 ? 4 : 1;
+    return (int64_t)counters_bytes(m) + (int64_t)ngroups * bmax * m->rows * 4;
+}
+
+extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
+                                void* y, hipStream_t stream) {
+    if (!valid_geometry(m)) return RANS_EGEOMETRY;
+    if (!valid_pointers(m) || !x || !y || batch <= 0) return RANS_EARG;
+    if (x_dtype != RANS_X_F32 && x_dtype != RANS_X_BF16) return RANS_EARG;
+    if (!supported_rs(m->R, m->S)) return RANS_EUNSUPPORTED;
+    const int waves = gemv_waves(m);
+    if (!waves) return RANS_EGEOMETRY;
+    const int ncb = m->cols / m->C;
+    const int ngroups = ncb / waves;
+    if (ngroups > 1 && (!m->workspace || m->workspace_bytes < rans_gemv_workspace_bytes(m, batch)))
+        return RANS_EWORKSPACE;
+    const bool xbf16 = x_dtype == RANS_X_BF16;
+    const size_t xsz = xbf16 ? 2 : 4;
+
+    GemvArgs a;
+    a.words = m->words;
+    a.tile_off = m->tile_off;
+    a.soffs = m->soffs;
+    a.states = m->states;
+    a.table = m->table;
+    a.esc_rowptr = m->esc_rowptr;
+    a.esc_col = m->esc_col;
+    a.esc_val = m->esc_val;
+    a.step = m->step;
+    a.rows = m->rows;
+    a.cols = m->cols;
+    a.C = m->C;
+    a.ncb = ncb;
+    a.ngroups = ngroups;
+    a.tile_lds_words = tile_lds_words(m);
+    a.counters = ngroups > 1 ? static_cast<uint32_t*>(m->workspace) : nullptr;
+    a.partial = ngroups > 1
+                    ? reinterpret_cast<float*>(static_cast<uint8_t*>(m->workspace) + counters_bytes(m))
+                    : nullptr;
+    const size_t lds = lds_bytes(waves, a.tile_lds_words);
+    const int grid = (m->rows / m->R) * ngroups;
+
+    // Batches run in chunks of 4 vectors, the remainder one vector at a time.
+    int done = 0;
+    while (done < batch) {
+        const int B = batch - done >= 4 ? 4 : 1;
+        a.x = static_cast<const uint8_t*>(x) + (size_t)done * m->cols * xsz;
+        a.y = static_cast<float*>(y) + (size_t)done * m->rows;
+        const int rc = dispatch_gemv(a, m->R, m->S, B, xbf16, waves, lds, grid, stream);
+        if (rc != 0) return rc;
+        done += B;
+    }
+    return 0;
+}
+
+extern "C" int launch_rans_decode(const rans_w64_matrix* m, void* out_bf16, hipStream_t stream) {
+    return launch_decode_common<1>(m, out_bf16, stream);
+}
+
+extern "C" int launch_rans_decode_codes(const rans_w64_matrix* m, int32_t* out, hipStream_t stream) {
+    return launch_decode_common<0>(m, out, stream);
+}
+
+extern "C" int launch_int4_gemv(const void* w, const void* x, void* y, int rows, int cols,
+                                hipStream_t stream) {
+    if (!w || !x || !y || rows <= 0 || cols <= 0) return RANS_EARG;
+    if (cols % 32) return RANS_EGEOMETRY;
+    hipLaunchKernelGGL(int4_gemv_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream,
+                       static_cast<const uint32_t*>(w), static_cast<const float*>(x),
+                       static_cast<float*>(y), rows, cols);
+    return (int)hipGetLastError();
+}

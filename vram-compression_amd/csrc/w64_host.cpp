@@ -1,0 +1,285 @@
+// Host side of the w64 stream format: static table build, the wavefront-
+// interleaved multi-state encoder, and a host decoder.  Plain C++17, no GPU
+// calls; built into librans_hip.so next to the kernels.
+//
+// The coder arithmetic is the reference's (kernel/rans.py:13-16, 62-98,
+// 101-123); the layout is this library's (see include/vramc_rans.h).
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "../../include/vramc_rans.h"
+
+namespace {
+
+constexpr uint32_t kScaleBits = 12;
+constexpr uint32_t kM = 1u << kScaleBits;
+constexpr uint32_t kRansL = 1u << 16;
+constexpr int kEsc = 0;
+
+struct Encoded {
+    std::vector<uint16_t> words;
+    std::vector<uint32_t> tile_off;
+    std::vector<uint16_t> soffs;
+    std::vector<uint32_t> states;
+    uint32_t table[kM];
+    int64_t freq[256];
+    std::vector<int32_t> esc_rowptr, esc_col, esc_val;
+    int64_t payload_words = 0;
+    int32_t max_tile_words = 0;
+};
+
+// Runs fn(i) for i in [0, n) on up to nthreads threads, static blocks.
+template <typename F>
+void parallel_for(int64_t n, int nthreads, F fn) {
+    if (nthreads <= 1 || n < 2) {
+        for (int64_t i = 0; i < n; i++) fn(i);
+        return;
+    }
+    nthreads = (int)std::min<int64_t>(nthreads, n);
+    std::vector<std::thread> pool;
+    for (int t = 0; t < nthreads; t++) {
+        pool.emplace_back([=, &fn] {
+            const int64_t lo = n * t / nthreads, hi = n * (t + 1) / nthreads;
+            for (int64_t i = lo; i < hi; i++) fn(i);
+        });
+    }
+    for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+extern "C" int rans_build_table(const uint8_t* sym, int64_t n, int64_t* freq, int64_t* cum,
+                                uint32_t* table) {
+    if (n <= 0 || !sym) return RANS_ECODES;
+    int64_t counts[256] = {0};
+    for (int64_t i = 0; i < n; i++) counts[sym[i]]++;
+    // Same quantisation as rans.py:36-44: round-half-even of count*M/total in
+    // double precision, floor of 1 for present symbols, then move the rounding
+    // residue onto the first largest bin.
+    int64_t sum = 0;
+    for (int s = 0; s < 256; s++) {
+        int64_t f = 0;
+        if (counts[s]) {
+            const double v = std::nearbyint(((double)counts[s] * (double)kM) / (double)n);
+            f = v < 1.0 ? 1 : (int64_t)v;
+        }
+        freq[s] = f;
+        sum += f;
+    }
+    while (sum != (int64_t)kM) {
+        const int64_t diff = (int64_t)kM - sum;
+        int big = 0;
+        for (int s = 1; s < 256; s++)
+            if (freq[s] > freq[big]) big = s;
+        const int64_t adj = diff < 0 ? std::max<int64_t>(diff, 1 - freq[big]) : diff;
+        freq[big] += adj;
+        sum += adj;
+    }
+    for (int s = 0; s < 256; s++)
+        if (freq[s] >= (int64_t)kM) return RANS_ECODES;
+    int64_t c = 0;
+    for (int s = 0; s < 256; s++) {
+        if (cum) cum[s] = c;
+        for (int64_t k = 0; k < freq[s]; k++)
+            table[c + k] = (uint32_t)s | ((uint32_t)freq[s] << 8) | ((uint32_t)k << 20);
+        c += freq[s];
+    }
+    return 0;
+}
+
+extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols, int32_t R,
+                               int32_t C, int32_t S, int32_t nthreads, void** handle,
+                               int64_t* info) {
+    if (!codes || !handle || !info || rows <= 0 || cols <= 0 || R <= 0 || C <= 0 || S <= 0)
+        return RANS_EARG;
+    if (rows % R || cols % C || C % (64 * S)) return RANS_EGEOMETRY;
+    const int64_t N = (int64_t)rows * cols;
+    auto* E = new Encoded();
+
+    // Symbols and the escape side table.
+    std::vector<uint8_t> sym((size_t)N);
+    E->esc_rowptr.assign((size_t)rows + 1, 0);
+    for (int32_t r = 0; r < rows; r++) {
+        const int32_t* row = codes + (int64_t)r * cols;
+        uint8_t* srow = sym.data() + (int64_t)r * cols;
+        for (int32_t c = 0; c < cols; c++) {
+            const int32_t v = row[c];
+            if (v >= -127 && v <= 127) {
+                srow[c] = (uint8_t)(v + 128);
+            } else {
+                srow[c] = kEsc;
+                E->esc_col.push_back(c);
+                E->esc_val.push_back(v);
+            }
+        }
+        E->esc_rowptr[(size_t)r + 1] = (int32_t)E->esc_col.size();
+    }
+
+    int64_t cum[256];
+    if (rans_build_table(sym.data(), N, E->freq, cum, E->table) != 0) {
+        delete E;
+        return RANS_ECODES;
+    }
+
+    const int32_t ncb = cols / C, nrb = rows / R;
+    const int64_t ntiles = (int64_t)nrb * ncb;
+    const int32_t nst = 64 * S;
+    const int32_t nk = C / nst;
+    const int64_t n = (int64_t)nk * R;  // symbols per state
+
+    std::vector<std::vector<uint16_t>> blocks((size_t)ntiles);
+    E->soffs.assign((size_t)(ntiles * nst), 0);
+    E->states.assign((size_t)(ntiles * nst), 0);
+    std::vector<int64_t> payload((size_t)ntiles, 0);
+    std::vector<int> too_big((size_t)ntiles, 0);
+
+    const int64_t* freq = E->freq;
+    parallel_for(ntiles, nthreads > 0 ? nthreads : 1, [&](int64_t t) {
+        const int32_t rb = (int32_t)(t / ncb), cb = (int32_t)(t % ncb);
+        std::vector<uint8_t> seq((size_t)n);
+        std::vector<uint16_t> emitted((size_t)n);
+        std::vector<uint16_t>& blk = blocks[(size_t)t];
+        blk.reserve((size_t)(n * nst / 4 + 16));
+        for (int32_t j = 0; j < nst; j++) {
+            const int32_t s = j / 64, l = j % 64;
+            int64_t i = 0;
+            for (int32_t k = 0; k < nk; k++) {
+                const int64_t col = (int64_t)cb * C + 64 * ((int64_t)S * k + s) + l;
+                for (int32_t r = 0; r < R; r++)
+                    seq[(size_t)i++] = sym[(size_t)(((int64_t)rb * R + r) * cols + col)];
+            }
+            // Reverse encode (rans.py:76-83): renormalise when x >= 2^20*f,
+            // then x = (x/f)<<12 + x%f + cum.  x stays below 2^32.
+            uint32_t x = kRansL;
+            int64_t cnt = 0;
+            for (int64_t q = n - 1; q >= 0; q--) {
+                const uint32_t f = (uint32_t)freq[seq[(size_t)q]];
+                const uint32_t c = (uint32_t)cum[seq[(size_t)q]];
+                if (x >= (f << 20)) {
+                    emitted[(size_t)cnt++] = (uint16_t)(x & 0xFFFF);
+                    x >>= 16;
+                }
+                x = ((x / f) << kScaleBits) + (x % f) + c;
+            }
+            const size_t sid = (size_t)(t * nst + j);
+            if (blk.size() > 65535) too_big[(size_t)t] = 1;
+            E->soffs[sid] = (uint16_t)blk.size();
+            E->states[sid] = x;
+            for (int64_t q = cnt - 1; q >= 0; q--) blk.push_back(emitted[(size_t)q]);
+            payload[(size_t)t] += cnt;
+        }
+        // At least one pad word (the decoder prefetches one word past the
+        // last one it consumes), then round up to 8 words (16-byte loads).
+        const size_t padded = (blk.size() + 1 + 7) & ~(size_t)7;
+        if (padded > 65535) too_big[(size_t)t] = 1;
+        blk.resize(padded, 0);
+    });
+    for (int64_t t = 0; t < ntiles; t++) {
+        if (too_big[(size_t)t]) {
+            delete E;
+            return RANS_ETILE;
+        }
+    }
+
+    E->tile_off.assign((size_t)ntiles + 1, 0);
+    int64_t total = 0;
+    for (int64_t t = 0; t < ntiles; t++) {
+        E->tile_off[(size_t)t] = (uint32_t)total;
+        total += (int64_t)blocks[(size_t)t].size();
+        E->max_tile_words = std::max<int32_t>(E->max_tile_words, (int32_t)blocks[(size_t)t].size());
+        E->payload_words += payload[(size_t)t];
+    }
+    if (total > 0xFFFFFFFFll) {
+        delete E;
+        return RANS_ETILE;
+    }
+    E->tile_off[(size_t)ntiles] = (uint32_t)total;
+    E->words.resize((size_t)total);
+    parallel_for(ntiles, nthreads > 0 ? nthreads : 1, [&](int64_t t) {
+        std::memcpy(E->words.data() + E->tile_off[(size_t)t], blocks[(size_t)t].data(),
+                    blocks[(size_t)t].size() * sizeof(uint16_t));
+    });
+
+    info[0] = total;
+    info[1] = ntiles;
+    info[2] = ntiles * nst;
+    info[3] = (int64_t)E->esc_col.size();
+    info[4] = E->max_tile_words;
+    info[5] = E->payload_words;
+    *handle = E;
+    return 0;
+}
+
+extern "C" int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off,
+                                     uint16_t* soffs, uint32_t* states, uint32_t* table,
+                                     int64_t* freq, int32_t* esc_rowptr, int32_t* esc_col,
+                                     int32_t* esc_val) {
+    if (!handle) return RANS_EARG;
+    auto* E = static_cast<Encoded*>(handle);
+    auto put = [](auto* dst, const auto& v) {
+        if (dst && !v.empty()) std::memcpy(dst, v.data(), v.size() * sizeof(v[0]));
+    };
+    put(words, E->words);
+    put(tile_off, E->tile_off);
+    put(soffs, E->soffs);
+    put(states, E->states);
+    put(esc_rowptr, E->esc_rowptr);
+    put(esc_col, E->esc_col);
+    put(esc_val, E->esc_val);
+    if (table) std::memcpy(table, E->table, sizeof(E->table));
+    if (freq) std::memcpy(freq, E->freq, sizeof(E->freq));
+    return 0;
+}
+
+extern "C" void rans_w64_encode_free(void* handle) { delete static_cast<Encoded*>(handle); }
+
+extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
+    if (!m || !out || !m->words || !m->tile_off || !m->soffs || !m->states || !m->table)
+        return RANS_EARG;
+    const int32_t rows = m->rows, cols = m->cols, R = m->R, C = m->C, S = m->S;
+    if (R <= 0 || C <= 0 || S <= 0 || rows % R || cols % C || C % (64 * S)) return RANS_EGEOMETRY;
+    const int32_t ncb = cols / C, nrb = rows / R, nst = 64 * S, nk = C / nst;
+    const int64_t ntiles = (int64_t)nrb * ncb;
+    const int64_t nwords = m->tile_off[ntiles];
+    for (int64_t t = 0; t < ntiles; t++) {
+        const int32_t rb = (int32_t)(t / ncb), cb = (int32_t)(t % ncb);
+        for (int32_t j = 0; j < nst; j++) {
+            const int32_t s = j / 64, l = j % 64;
+            const int64_t sid = t * nst + j;
+            uint32_t st = m->states[sid];
+            int64_t p = (int64_t)m->tile_off[t] + m->soffs[sid];
+            for (int32_t k = 0; k < nk; k++) {
+                const int64_t col = (int64_t)cb * C + 64 * ((int64_t)S * k + s) + l;
+                for (int32_t r = 0; r < R; r++) {
+                    const uint32_t e = m->table[st & (kM - 1)];
+                    st = ((e >> 8) & 0xFFFu) * (st >> kScaleBits) + (e >> 20);
+                    if (st < kRansL) {
+                        if (p >= nwords) return RANS_EARG;
+                        st = (st << 16) | m->words[p++];
+                    }
+                    out[((int64_t)rb * R + r) * cols + col] = (int32_t)(e & 0xFF) - 128;
+                }
+            }
+            if (st != kRansL) return (int)(sid + 1 > 0x7fffffff ? 0x7fffffff : sid + 1);
+        }
+    }
+    // The escape symbol decodes to kEsc-128; the side table must name exactly
+    // those positions.
+    int64_t nesc_stream = 0;
+    for (int64_t i = 0; i < (int64_t)rows * cols; i++) nesc_stream += out[i] == kEsc - 128;
+    const int64_t nesc = m->esc_rowptr ? m->esc_rowptr[rows] : 0;
+    if (nesc != nesc_stream) return RANS_EARG;
+    for (int32_t r = 0; r < rows && nesc; r++) {
+        for (int32_t e = m->esc_rowptr[r]; e < m->esc_rowptr[r + 1]; e++) {
+            if (m->esc_col[e] < 0 || m->esc_col[e] >= cols) return RANS_EARG;
+            int32_t* o = out + (int64_t)r * cols + m->esc_col[e];
+            if (*o != kEsc - 128) return RANS_EARG;
+            *o = m->esc_val[e];
+        }
+    }
+    return 0;
+}

@@ -1,0 +1,353 @@
+"""Host side of the wavefront-interleaved rANS GEMV for MI355X: table
+building, the w64 encoder and host decoder (C++ in librans_hip.so), and
+ctypes wrappers around the HIP kernels.
+
+Mirrors the interface of kernel/rans.py of snuri00/vram-compression:
+``build``, ``build_table``, ``lane_order``, ``encode``, ``decode_ref``,
+``RansMatrix`` (``.gemv``, ``.decode``, ``.nbytes``) and ``Int4Matrix``, with
+the same argument meaning and the same assert-on-error behaviour.  What
+changes is the stream layout (64-lane tiles, S states per lane, escapes), so
+``encode`` takes an extra ``S`` and accepts codes outside [-128, 127].
+
+PyTorch is used only for device buffers and streams; every GPU operation is
+a hand-written HIP kernel in librans_hip.so.  There is no CPU fallback:
+``RansMatrix`` raises when the library or a GPU is missing.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+LIB = os.path.join(HERE, "librans_hip.so")
+SOURCES = [os.path.join(CSRC, "rans_gemv.hip"), os.path.join(CSRC, "w64_host.cpp")]
+HEADERS = [os.path.join(INCLUDE, "vramc_rans.h")]
+
+SCALE_BITS = 12
+M = 1 << SCALE_BITS
+RANS_L = 1 << 16
+OFFSET = 128
+ESC = 0  # escape symbol: codes outside [-127, 127]
+LANES = 64
+
+X_F32, X_BF16 = 0, 1
+
+HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared",
+               # packed fp32 VALU ops stay disabled on this platform
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+class RansMatrixDesc(ctypes.Structure):
+    """ctypes mirror of rans_w64_matrix (include/vramc_rans.h)."""
+    _fields_ = [("rows", ctypes.c_int32), ("cols", ctypes.c_int32),
+                ("R", ctypes.c_int32), ("C", ctypes.c_int32), ("S", ctypes.c_int32),
+                ("max_tile_words", ctypes.c_int32),
+                ("words", ctypes.c_void_p), ("tile_off", ctypes.c_void_p),
+                ("soffs", ctypes.c_void_p), ("states", ctypes.c_void_p),
+                ("table", ctypes.c_void_p), ("esc_rowptr", ctypes.c_void_p),
+                ("esc_col", ctypes.c_void_p), ("esc_val", ctypes.c_void_p),
+                ("step", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
+                ("workspace_bytes", ctypes.c_int64)]
+
+
+EXPORTS = ("launch_rans_gemv", "rans_gemv_workspace_bytes", "launch_rans_decode",
+           "launch_rans_decode_codes", "launch_int4_gemv", "rans_build_table",
+           "rans_w64_encode", "rans_w64_encode_fetch", "rans_w64_encode_free",
+           "rans_w64_decode_host")
+
+
+def compile_lib(arch="gfx950", out=LIB):
+    """Compile librans_hip.so with hipcc for ``arch`` (always recompiles)."""
+    tmp = out + ".tmp"
+    cmd = ["hipcc", f"--offload-arch={arch}", *HIPCC_FLAGS, "-o", tmp, *SOURCES]
+    subprocess.check_call(cmd, stderr=subprocess.DEVNULL if os.environ.get("RANS_QUIET") else None)
+    os.replace(tmp, out)
+    return out
+
+
+def _stale(lib):
+    if not os.path.exists(lib):
+        return True
+    t = os.path.getmtime(lib)
+    return any(os.path.getmtime(s) > t for s in SOURCES + HEADERS)
+
+
+def load_lib(path=LIB):
+    """ctypes handle with argtypes set for every exported symbol; raises
+    AttributeError if one is missing (as rans.py:25-29 does)."""
+    lib = ctypes.CDLL(path)
+    P, I32, I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    D = ctypes.POINTER(RansMatrixDesc)
+    sig = {
+        "launch_rans_gemv": ([D, P, ctypes.c_int, ctypes.c_int, P, P], ctypes.c_int),
+        "rans_gemv_workspace_bytes": ([D, ctypes.c_int], I64),
+        "launch_rans_decode": ([D, P, P], ctypes.c_int),
+        "launch_rans_decode_codes": ([D, P, P], ctypes.c_int),
+        "launch_int4_gemv": ([P, P, P, ctypes.c_int, ctypes.c_int, P], ctypes.c_int),
+        "rans_build_table": ([P, I64, P, P, P], ctypes.c_int),
+        "rans_w64_encode": ([P, I32, I32, I32, I32, I32, I32, ctypes.POINTER(P), P], ctypes.c_int),
+        "rans_w64_encode_fetch": ([P] * 10, ctypes.c_int),
+        "rans_w64_encode_free": ([P], None),
+        "rans_w64_decode_host": ([D, P], ctypes.c_int),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(lib, name)
+        f.argtypes = args
+        f.restype = res
+    return lib
+
+
+_LIB = None
+
+
+def build(arch="gfx950"):
+    """Compile librans_hip.so when a source is newer than it (rans.py:19-30)
+    and return the ctypes handle."""
+    global _LIB
+    if _stale(LIB):
+        compile_lib(arch)
+        _LIB = None
+    if _LIB is None:
+        _LIB = load_lib(LIB)
+    return _LIB
+
+
+def _host_lib():
+    """The library for host-only calls (encoder, table, host decoder)."""
+    return _LIB if _LIB is not None else build()
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# --------------------------------------------------------------------- table
+def build_table(sym):
+    """sym: uint8 symbols.  Returns (freq[256], cum[256], table[4096]) with
+    12-bit probabilities, the quantisation of rans.py:34-51."""
+    s = np.ascontiguousarray(np.asarray(sym, np.uint8).ravel())
+    freq = np.zeros(256, np.int64)
+    cum = np.zeros(256, np.int64)
+    table = np.zeros(M, np.uint32)
+    rc = _host_lib().rans_build_table(_p(s), s.size, _p(freq), _p(cum), _p(table))
+    assert rc == 0, "degenerate distribution (single symbol)"
+    return freq, cum, table
+
+
+# ------------------------------------------------------------------ encoding
+def lane_order(sym, R, C, S=1):
+    """Symbols in decode order, one row per rANS state (rans.py:55-59 for the
+    64-lane layout): tile (rb, cb), state j = s*64 + l, symbol i = k*R + r is
+    sym[rb*R + r, cb*C + 64*(S*k + s) + l]."""
+    rows, cols = sym.shape
+    assert rows % R == 0 and cols % C == 0 and C % (LANES * S) == 0
+    a = sym.reshape(rows // R, R, cols // C, C // (LANES * S), S, LANES)  # rb r cb k s l
+    return a.transpose(0, 2, 4, 5, 3, 1).reshape(-1, (C // (LANES * S)) * R)
+
+
+def encode(codes, R, C, S=1, threads=None):
+    """codes: integer array (rows x cols), any range; values outside
+    [-127, 127] go through the escape side table.  Returns a dict with the
+    w64 stream and the bit accounting of rans.py:95-97:
+    bits_payload (renormalisation words), bits_state_offs (initial states,
+    per-state offsets, tile offsets and tile padding), bits_table (16 KB
+    table), bits_escape (side table)."""
+    codes = np.ascontiguousarray(codes, dtype=np.int32)
+    assert codes.ndim == 2 and codes.size > 0, "codes must be a non-empty matrix"
+    rows, cols = codes.shape
+    assert rows % R == 0 and cols % C == 0 and C % (LANES * S) == 0, \
+        "shape not divisible into R x C tiles with C % (64*S) == 0"
+    lib = _host_lib()
+    h = ctypes.c_void_p()
+    info = np.zeros(6, np.int64)
+    nthreads = threads or min(16, os.cpu_count() or 1)
+    rc = lib.rans_w64_encode(_p(codes), rows, cols, R, C, S, nthreads, ctypes.byref(h), _p(info))
+    assert rc != -5, "degenerate distribution (single symbol)"
+    assert rc != -6, "a tile needs more than 65535 words: use smaller R or C"
+    assert rc == 0, f"encode failed ({rc})"
+    nwords, ntiles, nstates, nesc, max_tile_words, payload_words = (int(v) for v in info)
+    words = np.zeros(nwords, np.uint16)
+    tile_off = np.zeros(ntiles + 1, np.uint32)
+    soffs = np.zeros(nstates, np.uint16)
+    states = np.zeros(nstates, np.uint32)
+    table = np.zeros(M, np.uint32)
+    freq = np.zeros(256, np.int64)
+    esc_rowptr = np.zeros(rows + 1, np.int32)
+    esc_col = np.zeros(nesc, np.int32)
+    esc_val = np.zeros(nesc, np.int32)
+    try:
+        rc = lib.rans_w64_encode_fetch(h, _p(words), _p(tile_off), _p(soffs), _p(states),
+                                       _p(table), _p(freq), _p(esc_rowptr), _p(esc_col),
+                                       _p(esc_val))
+        assert rc == 0
+    finally:
+        lib.rans_w64_encode_free(h)
+    N = codes.size
+    sym = np.where((codes >= -127) & (codes <= 127), codes + OFFSET, ESC).astype(np.uint8)
+    p = freq[sym.ravel()] / M
+    pad_words = nwords - payload_words
+    return dict(words=words, tile_off=tile_off, soffs=soffs, states=states, table=table,
+                esc_rowptr=esc_rowptr, esc_col=esc_col, esc_val=esc_val,
+                R=R, C=C, S=S, shape=codes.shape, max_tile_words=max_tile_words,
+                bits_payload=16 * payload_words / N,
+                bits_state_offs=(48 * nstates + 32 * (ntiles + 1) + 16 * pad_words) / N,
+                bits_table=32 * M / N,
+                bits_escape=32 * (rows + 1 + 2 * nesc) / N,
+                entropy_model=float(-np.log2(p).mean()))
+
+
+def _host_desc(enc, keep):
+    """rans_w64_matrix over host numpy arrays (for rans_w64_decode_host)."""
+    arrs = {k: np.ascontiguousarray(enc[k]) for k in
+            ("words", "tile_off", "soffs", "states", "table", "esc_rowptr", "esc_col", "esc_val")}
+    keep.append(arrs)
+    rows, cols = enc["shape"]
+    d = RansMatrixDesc(rows=rows, cols=cols, R=enc["R"], C=enc["C"], S=enc["S"],
+                       max_tile_words=enc["max_tile_words"])
+    for k, a in arrs.items():
+        setattr(d, k, a.ctypes.data if a.size else None)
+    return d
+
+
+def decode_ref(enc):
+    """Host decoder of the w64 stream (rans.py:101-123 semantics): returns
+    int64 codes (rows x cols), escapes applied; asserts that every state
+    returns to 2^16 and that the escape side table matches the stream."""
+    rows, cols = enc["shape"]
+    keep = []
+    d = _host_desc(enc, keep)
+    out = np.zeros((rows, cols), np.int32)
+    rc = _host_lib().rans_w64_decode_host(ctypes.byref(d), _p(out))
+    assert rc <= 0, f"stream did not return to initial state (state {rc - 1})"
+    assert rc == 0, f"corrupt stream or escape side table ({rc})"
+    return out.astype(np.int64)
+
+
+# ------------------------------------------------------------------- device
+def _require_gpu():
+    if not torch.cuda.is_available():
+        raise RuntimeError("RansMatrix needs a ROCm GPU (gfx950); no CPU fallback exists")
+
+
+class RansMatrix:
+    """Entropy-coded matrix resident on the GPU (rans.py:127-162)."""
+
+    def __init__(self, enc, step, lib):
+        _require_gpu()
+        if lib is None:
+            raise RuntimeError("librans_hip.so not loaded")
+        self.lib = lib
+        self.R, self.C, self.S = enc["R"], enc["C"], enc["S"]
+        self.rows, self.cols = enc["shape"]
+        dev = torch.device("cuda")
+
+        def up(a, dt):
+            return torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(dev)
+
+        self.words = up(enc["words"], np.int16)
+        self.tile_off = up(enc["tile_off"], np.int32)
+        self.soffs = up(enc["soffs"], np.int16)
+        self.states = up(enc["states"], np.int32)
+        self.table = up(enc["table"], np.int32)
+        self.esc_rowptr = up(enc["esc_rowptr"], np.int32)
+        # never hand a zero-length buffer's (possibly null) pointer to the ABI
+        self.esc_col = up(enc["esc_col"] if len(enc["esc_col"]) else np.zeros(1, np.int32), np.int32)
+        self.esc_val = up(enc["esc_val"] if len(enc["esc_val"]) else np.zeros(1, np.int32), np.int32)
+        step = torch.as_tensor(step)
+        assert step.numel() == self.cols, "step must have one value per column"
+        self.step = step.float().reshape(self.cols).contiguous().to(dev)
+        self.max_tile_words = int(enc["max_tile_words"])
+        self._desc = RansMatrixDesc(
+            rows=self.rows, cols=self.cols, R=self.R, C=self.C, S=self.S,
+            max_tile_words=self.max_tile_words,
+            words=self.words.data_ptr(), tile_off=self.tile_off.data_ptr(),
+            soffs=self.soffs.data_ptr(), states=self.states.data_ptr(),
+            table=self.table.data_ptr(), esc_rowptr=self.esc_rowptr.data_ptr(),
+            esc_col=self.esc_col.data_ptr(), esc_val=self.esc_val.data_ptr(),
+            step=self.step.data_ptr(), workspace=None, workspace_bytes=0)
+        self.workspace = None
+        self._ensure_workspace(4)
+        self.nbytes = sum(t.numel() * t.element_size() for t in
+                          (self.words, self.tile_off, self.soffs, self.states, self.table,
+                           self.esc_rowptr)) + 8 * int(len(enc["esc_col"]))
+
+    def _ensure_workspace(self, batch):
+        need = int(self.lib.rans_gemv_workspace_bytes(ctypes.byref(self._desc), batch))
+        assert need >= 0, f"tile geometry not launchable ({need})"
+        if need and (self.workspace is None or self.workspace.numel() < need):
+            # zero once: the kernel keeps its counters at zero between launches
+            self.workspace = torch.zeros(need, dtype=torch.uint8, device="cuda")
+            self._desc.workspace = self.workspace.data_ptr()
+            self._desc.workspace_bytes = need
+
+    def gemv(self, x, y=None):
+        """y = codes @ (x * step) for x of shape (cols,) or (B, cols), f32 or
+        bf16; returns f32 (rows,) or (B, rows).  The step fold runs inside
+        the kernel."""
+        assert x.is_cuda, "x must be a device tensor"
+        squeeze = x.dim() == 1
+        xb = x.reshape(1, -1) if squeeze else x
+        assert xb.shape[-1] == self.cols
+        if xb.dtype == torch.bfloat16:
+            xd = X_BF16
+        else:
+            xb, xd = xb.float(), X_F32
+        xb = xb.contiguous()
+        B = xb.shape[0]
+        if y is None:
+            y = torch.empty((B, self.rows) if not squeeze else (self.rows,),
+                            device="cuda", dtype=torch.float32)
+        assert y.dtype == torch.float32 and y.is_contiguous() and y.numel() == B * self.rows
+        rc = self.lib.launch_rans_gemv(ctypes.byref(self._desc), xb.data_ptr(), xd, B,
+                                       y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, f"HIP error {rc}"
+        return y
+
+    def decode(self, out=None):
+        """Dense bf16 rows x cols matrix code*step (rans.py:154-162)."""
+        if out is None:
+            out = torch.empty(self.rows, self.cols, device="cuda", dtype=torch.bfloat16)
+        assert out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == self.rows * self.cols
+        rc = self.lib.launch_rans_decode(ctypes.byref(self._desc), out.data_ptr(),
+                                         torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, f"HIP error {rc}"
+        return out
+
+    def decode_codes(self, out=None):
+        """Dense int32 codes on the GPU, escapes included (bit-exact path)."""
+        if out is None:
+            out = torch.empty(self.rows, self.cols, device="cuda", dtype=torch.int32)
+        assert out.dtype == torch.int32 and out.is_contiguous() and out.numel() == self.rows * self.cols
+        rc = self.lib.launch_rans_decode_codes(ctypes.byref(self._desc), out.data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, f"HIP error {rc}"
+        return out
+
+
+class Int4Matrix:
+    """Fixed-rate 4-bit baseline (codes in [-8, 7]), rans.py:165-185."""
+
+    def __init__(self, codes, step, lib):
+        _require_gpu()
+        self.lib = lib
+        self.rows, self.cols = codes.shape
+        assert self.cols % 32 == 0, "cols must be a multiple of 32"
+        q = (np.clip(codes, -8, 7) + 8).astype(np.uint32).reshape(self.rows, -1, 8)
+        packed = np.zeros(q.shape[:2], np.uint32)
+        for b in range(8):
+            packed |= q[:, :, b] << np.uint32(4 * b)
+        self.w = torch.from_numpy(packed.view(np.int32)).cuda()
+        self.step = torch.as_tensor(step).float().cuda()
+        self.nbytes = self.w.numel() * 4
+
+    def gemv(self, x, y=None):
+        xs = (x.float() * self.step).contiguous()
+        y = torch.empty(self.rows, device="cuda") if y is None else y
+        rc = self.lib.launch_int4_gemv(self.w.data_ptr(), xs.data_ptr(), y.data_ptr(),
+                                       self.rows, self.cols, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, f"HIP error {rc}"
+        return y
