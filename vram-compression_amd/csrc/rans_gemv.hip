@@ -73,18 +73,41 @@ struct DecodeArgs {
 
 // Expands the reference-packed table (sym | freq<<8 | bias<<20) into LDS
 // pairs {freq | code<<24, bias}; the escape symbol (0) gets code 0 so it adds
-// nothing in the GEMV and is patched from the side table afterwards.
+// nothing in the GEMV and is patched from the side table afterwards.  All
+// 16-byte loads of a thread are issued before the first LDS write, so the
+// workgroup pays one memory latency, not one per loop trip.
+__device__ inline uint2 expand_entry(uint32_t e) {
+    const uint32_t sym = e & 0xFFu;
+    const uint32_t code = sym == 0 ? 0u : (uint32_t)((int32_t)sym - 128);
+    return make_uint2(((e >> 8) & 0xFFFu) | (code << 24), e >> 20);
+}
+
 __device__ inline void stage_table(uint2* tab, const uint32_t* __restrict__ table) {
-    for (int i = threadIdx.x; i < (int)kProbM; i += blockDim.x) {
-        const uint32_t e = table[i];
-        const uint32_t sym = e & 0xFFu;
-        const uint32_t code = sym == 0 ? 0u : (uint32_t)((int32_t)sym - 128);
-        tab[i] = make_uint2(((e >> 8) & 0xFFFu) | (code << 24), e >> 20);
+    const uint4* src = reinterpret_cast<const uint4*>(table);  // 1024 x 16 B
+    const int n = blockDim.x;                                   // 64 .. 512
+    uint4 v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        // clamped, unconditional loads: a guarded load becomes a branch with
+        // its own wait
+        const int i = min((int)threadIdx.x + j * n, 1023);
+        v[j] = src[i];
+    }
+    // Clamped indices repeat the last entry's write with the same value,
+    // which keeps the stores branch-free (and the loads un-sunk).
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int i = min((int)threadIdx.x + j * n, 1023);
+        tab[4 * i + 0] = expand_entry(v[j].x);
+        tab[4 * i + 1] = expand_entry(v[j].y);
+        tab[4 * i + 2] = expand_entry(v[j].z);
+        tab[4 * i + 3] = expand_entry(v[j].w);
     }
 }
 
 // Copies tile t's compressed block (a multiple of 8 words) into this wave's
-// LDS region with 16-byte loads; never writes past max_words.
+// LDS region with 16-byte loads, 8 per lane in flight at a time; never
+// writes past max_words.
 __device__ inline void stage_tile(uint16_t* tw, const uint16_t* __restrict__ words,
                                   const uint32_t* __restrict__ tile_off, int t, int lane,
                                   int max_words) {
@@ -93,7 +116,18 @@ __device__ inline void stage_tile(uint16_t* tw, const uint16_t* __restrict__ wor
     if (nw > (uint32_t)max_words) nw = (uint32_t)max_words;
     const uint4* src = reinterpret_cast<const uint4*>(words + o0);
     uint4* dst = reinterpret_cast<uint4*>(tw);
-    for (uint32_t i = lane; i < (nw >> 3); i += 64) dst[i] = src[i];
+    const uint32_t n16 = nw >> 3;
+    if (n16 == 0) return;
+    for (uint32_t b = 0; b < n16; b += 64 * 8) {
+        uint4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t i = min(b + lane + 64 * j, n16 - 1);  // n16 >= 1
+            v[j] = src[i];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) dst[min(b + lane + 64 * j, n16 - 1)] = v[j];
+    }
 }
 
 __device__ inline float load_x(const void* x, int64_t i, bool bf16) {
@@ -102,6 +136,15 @@ __device__ inline float load_x(const void* x, int64_t i, bool bf16) {
         return __uint_as_float(v << 16);
     }
     return reinterpret_cast<const float*>(x)[i];
+}
+
+__device__ inline uint32_t load_x_bits(const void* x, int64_t i, bool bf16) {
+    if (bf16) return reinterpret_cast<const uint16_t*>(x)[i];
+    return reinterpret_cast<const uint32_t*>(x)[i];
+}
+
+__device__ inline float bits_to_x(uint32_t v, bool bf16) {
+    return __uint_as_float(bf16 ? v << 16 : v);
 }
 
 __device__ inline float wave_sum(float v) {
@@ -167,23 +210,57 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         for (int s = 0; s < S; s++) w[s] = tw[p[s]];
         const int nk = a.C / (64 * S);
         const int colbase = cb * a.C + lane;
-        for (int k = 0; k < nk; k++) {
-            float xv[S][B];
+        // x and step for KU column steps are loaded one block ahead of use,
+        // so their latency overlaps the decode of the current block.
+        constexpr int KU = 4;
+        uint32_t xr[KU][S][B];  // raw bits: bf16 zero-extended, or f32
+        float sr[KU][S];
+        auto load_block = [&](int k0) {
 #pragma unroll
-            for (int s = 0; s < S; s++) {
-                const int col = colbase + 64 * (S * k + s);
-                const float sc = a.step[col];
-#pragma unroll
-                for (int b = 0; b < B; b++)
-                    xv[s][b] = load_x(a.x, (int64_t)b * a.cols + col, XBF16) * sc;
-            }
-#pragma unroll
-            for (int r = 0; r < R; r++) {
+            for (int u = 0; u < KU; u++) {
+                const int k = k0 + u < nk ? k0 + u : nk - 1;
 #pragma unroll
                 for (int s = 0; s < S; s++) {
-                    const float code = (float)rans_step(st[s], p[s], w[s], tab, tw);
+                    const int col = colbase + 64 * (S * k + s);
+                    sr[u][s] = a.step[col];
 #pragma unroll
-                    for (int b = 0; b < B; b++) acc[r][b] = fmaf(code, xv[s][b], acc[r][b]);
+                    for (int b = 0; b < B; b++)
+                        xr[u][s][b] = load_x_bits(a.x, (int64_t)b * a.cols + col, XBF16);
+                }
+            }
+        };
+        load_block(0);
+        for (int k0 = 0; k0 < nk; k0 += KU) {
+            float xv[KU][S][B];
+#pragma unroll
+            for (int u = 0; u < KU; u++)
+#pragma unroll
+                for (int s = 0; s < S; s++) {
+                    // pin the use of the prefetched registers here (top of the
+                    // block) so the multiply is not hoisted next to the loads
+                    asm volatile("" : "+v"(sr[u][s]));
+#pragma unroll
+                    for (int b = 0; b < B; b++) {
+                        asm volatile("" : "+v"(xr[u][s][b]));
+                        xv[u][s][b] = bits_to_x(xr[u][s][b], XBF16) * sr[u][s];
+                    }
+                }
+            if (k0 + KU < nk) load_block(k0 + KU);
+            // keep the prefetch here: without this the scheduler sinks the
+            // loads below the decode and the next block waits on them
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < KU; u++) {
+                if (k0 + u >= nk) break;
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+#pragma unroll
+                    for (int s = 0; s < S; s++) {
+                        const float code = (float)rans_step(st[s], p[s], w[s], tab, tw);
+#pragma unroll
+                        for (int b = 0; b < B; b++)
+                            acc[r][b] = fmaf(code, xv[u][s][b], acc[r][b]);
+                    }
                 }
             }
         }
@@ -241,19 +318,24 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
 
     // Split over column groups: publish the partial, count arrivals, and let
     // the last workgroup of this tile row sum the partials in group order.
+    // Partials are written with agent-scope atomic stores, which write
+    // through the per-XCD L2, and every thread waits for its store to
+    // complete before the barrier; the arrival counter is then bumped and
+    // the last workgroup reads the partials with agent-scope (coherent)
+    // loads.  This avoids release/acquire fences, which on this chip write
+    // back or invalidate the whole L2 of the XCD.
     if (tid < R * B)
         __hip_atomic_store(&a.partial[((int64_t)g * B + b) * a.rows + row], v, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
-    __threadfence();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(&a.counters[rb], 1u, __ATOMIC_ACQ_REL,
+        const uint32_t old = __hip_atomic_fetch_add(&a.counters[rb], 1u, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT);
         *flag = old == (uint32_t)(a.ngroups - 1);
     }
     __syncthreads();
     if (*flag) {
-        __threadfence();
         if (tid < R * B) {
             float s = 0.f;
             for (int gg = 0; gg < a.ngroups; gg++)
