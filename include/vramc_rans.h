@@ -66,6 +66,9 @@ typedef struct rans_w64_matrix {
     int32_t rows, cols;       /* out_features, in_features */
     int32_t R, C, S;          /* tile rows, tile columns, states per lane */
     int32_t max_tile_words;   /* largest tile block, in 16-bit words */
+    int32_t max_state_words;  /* longest state stream (to the next state's start, the
+                                 last state of a tile to the end of its padded block) */
+    int32_t reserved;         /* keeps the pointers 8-byte aligned; set to 0 */
     const uint16_t* words;    /* [tile_off[ntiles]] */
     const uint32_t* tile_off; /* [ntiles+1], in words, multiples of 8 */
     const uint16_t* soffs;    /* [ntiles*64*S] */
@@ -119,7 +122,8 @@ int rans_build_table(const uint8_t* sym, int64_t n, int64_t* freq, int64_t* cum,
 
 /* Encode int32 codes (rows x cols, row-major) into the w64 format; replaces
  * encode() (rans.py:62-98).  On success *handle owns the result and info[]
- * receives {nwords, ntiles, nstates, nesc, max_tile_words, payload_words}.
+ * receives {nwords, ntiles, nstates, nesc, max_tile_words, payload_words,
+ * max_state_words}.
  * Fetch the arrays with rans_w64_encode_fetch, then free the handle. */
 int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols, int32_t R, int32_t C,
                     int32_t S, int32_t nthreads, void** handle, int64_t* info);

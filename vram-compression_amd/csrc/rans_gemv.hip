@@ -7,13 +7,17 @@
 //      slot-cum} pairs, so one ds_read_b64 yields both rANS operands and the
 //      signed code (the reference keeps sym|freq<<8|bias<<20 and extracts the
 //      fields with three more ALU ops per symbol, rans_gemv.cu:33-36);
-//   2. each wavefront copies its tile's whole compressed block into its own
-//      LDS region with 16-byte loads (coalesced across the 64 lanes), so the
-//      data-dependent renormalisation reads hit LDS, not HBM;
-//   3. each lane runs S independent rANS states; per column step k a lane
-//      loads x[c]*step[c] once (the waterfilling fold happens here) and
-//      reuses it for the R rows of the tile;
-//   4. row sums are reduced across the 64 lanes with cross-lane shuffles and
+//   2. each wavefront copies its tile's compressed block into LDS with
+//      16-byte loads (coalesced across the 64 lanes), issued together with
+//      the table loads so both latencies overlap;
+//   3. inside LDS each lane re-lays its states' word streams column-wise
+//      (word i of state j at row i, column j): the data-dependent
+//      renormalisation reads of the 64 lanes then fall into a few adjacent
+//      rows (at most 2-way bank conflicts) instead of 64 random addresses;
+//   4. each lane runs S independent rANS states; per column step a lane
+//      loads x[c]*step[c] once (the waterfilling fold happens here, one block
+//      of column steps ahead of use) and reuses it for the R rows of the tile;
+//   5. row sums are reduced across the 64 lanes with cross-lane shuffles and
 //      across the W waves through LDS in a fixed order, escapes are added
 //      from the CSR side table, and y is written; when one workgroup does not
 //      cover all column tiles, partial sums go to a workspace and the last
@@ -33,15 +37,28 @@ constexpr uint32_t kRansL = 1u << 16;
 constexpr int kMaxWaves = 8;
 constexpr int kMaxRB = 64;  // largest R*B compiled (16 * 4)
 
-// LDS layout of the GEMV/decode kernels (bytes).
-constexpr int kTabOff = 0;                          // uint2[4096]
-constexpr int kRedOff = kTabOff + 8 * (int)kProbM;  // float[kMaxWaves*kMaxRB]
-constexpr int kEscOff = kRedOff + 4 * kMaxWaves * kMaxRB;  // float[kMaxRB]
-constexpr int kFlagOff = kEscOff + 4 * kMaxRB;      // int
-constexpr int kTileOff = kFlagOff + 16;             // per-wave tile regions
+// LDS: the expanded table and the reduction scratch are static __shared__
+// arrays (their offsets are compile-time constants, so table addressing
+// needs no base add); the per-wave regions are dynamic.
+constexpr int kStaticLds = 8 * (int)kProbM + 4 * kMaxWaves * kMaxRB + 4 * kMaxRB + 16;
 constexpr int kLdsMax = 160 * 1024;
 
-static_assert(kTileOff % 16 == 0, "tile regions must be 16-byte aligned");
+// 32-bit LDS addresses (address space 3), so a word read is one ds_read with
+// no base arithmetic.
+using lds_cu16 = const __attribute__((address_space(3))) uint16_t;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ uint32_t lds_read_u16(uint32_t a) {
+    return *(lds_cu16*)(uintptr_t)a;
+}
+
+// Per-wave LDS region, in 16-bit words: the staged tile block plus one
+// read-ahead word past its end.
+struct WaveLayout {
+    int raw_words;   // multiple of 8
+    int wave_words;  // = raw_words
+};
 
 struct GemvArgs {
     const uint16_t* words;
@@ -57,7 +74,8 @@ struct GemvArgs {
     float* y;
     float* partial;      // [ngroups][B][rows]
     uint32_t* counters;  // [rows/R]
-    int rows, cols, C, ncb, ngroups, tile_lds_words;
+    int rows, cols, C, ncb, ngroups;
+    WaveLayout L;
 };
 
 struct DecodeArgs {
@@ -68,118 +86,161 @@ struct DecodeArgs {
     const uint32_t* table;
     const float* step;
     void* out;
-    int rows, cols, C, ncb, ntiles, tile_lds_words;
+    int rows, cols, C, ncb, ntiles;
+    WaveLayout L;
 };
 
-// Expands the reference-packed table (sym | freq<<8 | bias<<20) into LDS
-// pairs {freq | code<<24, bias}; the escape symbol (0) gets code 0 so it adds
-// nothing in the GEMV and is patched from the side table afterwards.  All
-// 16-byte loads of a thread are issued before the first LDS write, so the
-// workgroup pays one memory latency, not one per loop trip.
-__device__ inline uint2 expand_entry(uint32_t e) {
+// Reference-packed table entry (sym | freq<<8 | bias<<20) -> LDS pair
+// {freq | code<<24, bias}; the escape symbol (0) gets code 0 so it adds
+// nothing in the GEMV and is patched from the side table.
+__device__ __forceinline__ uint2 expand_entry(uint32_t e) {
     const uint32_t sym = e & 0xFFu;
     const uint32_t code = sym == 0 ? 0u : (uint32_t)((int32_t)sym - 128);
     return make_uint2(((e >> 8) & 0xFFFu) | (code << 24), e >> 20);
 }
 
-__device__ inline void stage_table(uint2* tab, const uint32_t* __restrict__ table) {
-    const uint4* src = reinterpret_cast<const uint4*>(table);  // 1024 x 16 B
-    const int n = blockDim.x;                                   // 64 .. 512
-    uint4 v[16];
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-        // clamped, unconditional loads: a guarded load becomes a branch with
-        // its own wait
-        const int i = min((int)threadIdx.x + j * n, 1023);
-        v[j] = src[i];
-    }
-    // Clamped indices repeat the last entry's write with the same value,
-    // which keeps the stores branch-free (and the loads un-sunk).
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-        const int i = min((int)threadIdx.x + j * n, 1023);
-        tab[4 * i + 0] = expand_entry(v[j].x);
-        tab[4 * i + 1] = expand_entry(v[j].y);
-        tab[4 * i + 2] = expand_entry(v[j].z);
-        tab[4 * i + 3] = expand_entry(v[j].w);
-    }
+// Keeps the four registers of v live here: the loads that produce them
+// cannot be sunk below this point (next to the stores that use them).
+__device__ __forceinline__ void pin(const uint4& v) {
+    asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
 }
 
-// Copies tile t's compressed block (a multiple of 8 words) into this wave's
-// LDS region with 16-byte loads, 8 per lane in flight at a time; never
-// writes past max_words.
-__device__ inline void stage_tile(uint16_t* tw, const uint16_t* __restrict__ words,
-                                  const uint32_t* __restrict__ tile_off, int t, int lane,
-                                  int max_words) {
-    const uint32_t o0 = tile_off[t];
-    uint32_t nw = tile_off[t + 1] - o0;
-    if (nw > (uint32_t)max_words) nw = (uint32_t)max_words;
-    const uint4* src = reinterpret_cast<const uint4*>(words + o0);
-    uint4* dst = reinterpret_cast<uint4*>(tw);
-    const uint32_t n16 = nw >> 3;
-    if (n16 == 0) return;
-    for (uint32_t b = 0; b < n16; b += 64 * 8) {
-        uint4 v[8];
+// Stages the expanded table (whole workgroup) and, for an active wave, its
+// tile block (a multiple of 8 words, at most raw_words) into LDS.  The
+// table loads and the first batch of tile loads are all issued before the
+// first LDS write, so the workgroup pays one memory latency.  Loads use
+// clamped indices (unconditional: a guarded load becomes a branch with its
+// own wait); stores are guarded, so no two lanes store to one address.
+__device__ __forceinline__ void stage_table_and_tile(uint2* tab, const uint32_t* __restrict__ table,
+                                                     uint16_t* raw,
+                                                     const uint16_t* __restrict__ words,
+                                                     const uint32_t* __restrict__ tile_off, int t,
+                                                     bool active, int lane, int raw_words) {
+    const uint4* tsrc = reinterpret_cast<const uint4*>(table);  // 1024 x 16 B
+    const int n = blockDim.x;                                    // 64 .. 512
+    const int tid = threadIdx.x;
+    uint4 tv[16];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t i = min(b + lane + 64 * j, n16 - 1);  // n16 >= 1
-            v[j] = src[i];
+    for (int j = 0; j < 16; j++) tv[j] = tsrc[min(tid + j * n, 1023)];
+
+    // tile extent, made explicitly wave-uniform (scalar loop control)
+    uint32_t o0 = 0, n16 = 0;
+    if (active) {
+        o0 = tile_off[t];
+        uint32_t nw = tile_off[t + 1] - o0;
+        if (nw > (uint32_t)raw_words) nw = (uint32_t)raw_words;
+        n16 = nw >> 3;
+    }
+    o0 = __builtin_amdgcn_readfirstlane(o0);
+    n16 = __builtin_amdgcn_readfirstlane(n16);
+    const uint4* src = reinterpret_cast<const uint4*>(words + o0);
+    uint4* dst = reinterpret_cast<uint4*>(raw);
+    uint4 v[8];
+    if (n16) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = src[min((uint32_t)(lane + 64 * j), n16 - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; j++) pin(tv[j]);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int i = tid + j * n;
+        if (i < 1024) {
+            tab[4 * i + 0] = expand_entry(tv[j].x);
+            tab[4 * i + 1] = expand_entry(tv[j].y);
+            tab[4 * i + 2] = expand_entry(tv[j].z);
+            tab[4 * i + 3] = expand_entry(tv[j].w);
+        }
+    }
+    for (uint32_t b = 0; b < n16; b += 512) {
+        if (b) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = src[min(b + lane + 64 * j, n16 - 1)];
         }
 #pragma unroll
-        for (int j = 0; j < 8; j++) dst[min(b + lane + 64 * j, n16 - 1)] = v[j];
+        for (int j = 0; j < 8; j++) pin(v[j]);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t i = b + lane + 64 * j;
+            if (i < n16) dst[i] = v[j];
+        }
     }
 }
 
-__device__ inline float load_x(const void* x, int64_t i, bool bf16) {
-    if (bf16) {
-        const uint32_t v = reinterpret_cast<const uint16_t*>(x)[i];
-        return __uint_as_float(v << 16);
-    }
-    return reinterpret_cast<const float*>(x)[i];
-}
-
-__device__ inline uint32_t load_x_bits(const void* x, int64_t i, bool bf16) {
+__device__ __forceinline__ uint32_t load_x_bits(const void* x, int64_t i, bool bf16) {
     if (bf16) return reinterpret_cast<const uint16_t*>(x)[i];
     return reinterpret_cast<const uint32_t*>(x)[i];
 }
 
-__device__ inline float bits_to_x(uint32_t v, bool bf16) {
+__device__ __forceinline__ float bits_to_x(uint32_t v, bool bf16) {
     return __uint_as_float(bf16 ? v << 16 : v);
 }
 
-__device__ inline float wave_sum(float v) {
+__device__ __forceinline__ float load_x(const void* x, int64_t i, bool bf16) {
+    return bits_to_x(load_x_bits(x, i, bf16), bf16);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
 
+// Per-lane decoder state of S interleaved rANS states, with the table entry
+// of each state's next symbol already read (software pipelined: the read for
+// symbol i+1 is issued before the GEMV work of symbol i).
+template <int S>
+struct Lanes {
+    uint32_t st[S];  // rANS states
+    uint32_t a[S];   // LDS byte address of the next unread word of each state
+    uint32_t w[S];   // that word (read ahead)
+    uint2 e[S];      // table entry for the next symbol of each state
+};
+
+// Staged-block setup: each state's read pointer, its first word and the
+// table entry of its first symbol.  Call after the staging barrier.
+template <int S>
+__device__ __forceinline__ void init_lanes(Lanes<S>& L, const uint2* tab, const uint16_t* raw,
+                                           const uint32_t (&st0)[S], const uint32_t (&off0)[S]) {
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        L.st[s] = st0[s];
+        L.a[s] = lds_addr(raw + off0[s]);
+        L.w[s] = lds_read_u16(L.a[s]);
+        L.e[s] = tab[L.st[s] & (kProbM - 1)];
+    }
+}
+
 // One rANS decode step with the reference arithmetic (rans_gemv.cu:32-37):
-// e = tab[st & 4095]; st = freq*(st>>12) + bias; renormalise from the LDS
-// word stream when st < 2^16.  w holds the next unread word of the stream
-// (prefetched), p its index in the wave's LDS region.
-__device__ inline int32_t rans_step(uint32_t& st, uint32_t& p, uint32_t& w, const uint2* tab,
-                                    const uint16_t* tw) {
-    const uint2 e = tab[st & (kProbM - 1)];
-    const uint32_t ns = __umul24(e.x, st >> 12) + e.y;  // freq < 2^12, st>>12 < 2^20
+// st = freq*(st>>12) + bias from the entry e = tab[st & 4095]; renormalise
+// with the next stream word when st < 2^16; return the symbol's code.  The
+// entry for the following symbol is read as soon as the new state exists,
+// before the code conversion and the word-pointer update, so those overlap
+// the LDS latency instead of sitting on the state's dependency chain.
+__device__ __forceinline__ int32_t rans_step(uint32_t& st, uint32_t& a, uint32_t& w, uint2& e,
+                                             const uint2* tab) {
+    const uint2 cur = e;
+    const uint32_t ns = __umul24(cur.x, st >> 12) + cur.y;  // freq < 2^12, st>>12 < 2^20
     const bool need = ns < kRansL;
-    const uint32_t rn = (ns << 16) | w;
-    st = need ? rn : ns;
-    p += need ? 1u : 0u;
-    w = tw[p];
-    return (int32_t)e.x >> 24;
+    st = need ? ((ns << 16) | w) : ns;
+    e = tab[st & (kProbM - 1)];
+    a += need ? 2u : 0u;
+    w = lds_read_u16(a);
+    return (int32_t)cur.x >> 24;
 }
 
 template <int R, int S, int B, bool XBF16>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs a) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    uint2* tab = reinterpret_cast<uint2*>(lds + kTabOff);
-    float* red = reinterpret_cast<float*>(lds + kRedOff);
-    float* esc_red = reinterpret_cast<float*>(lds + kEscOff);
-    int* flag = reinterpret_cast<int*>(lds + kFlagOff);
+    __shared__ __align__(16) uint2 tab[kProbM];
+    __shared__ float red[kMaxWaves * kMaxRB];
+    __shared__ float esc_red[kMaxRB];
+    __shared__ int flag[4];
+    extern __shared__ __align__(16) uint16_t dyn[];
+    constexpr int nst = 64 * S;
     const int W = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar tile math
     const int lane = threadIdx.x & 63;
-    uint16_t* tw = reinterpret_cast<uint16_t*>(lds + kTileOff) + (size_t)wave * a.tile_lds_words;
+    uint16_t* raw = dyn + (size_t)wave * a.L.wave_words;
 
     const int rb = blockIdx.x / a.ngroups;
     const int g = blockIdx.x - rb * a.ngroups;
@@ -187,8 +248,40 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     const bool active = cb < a.ncb;
     const int t = rb * a.ncb + cb;
 
-    stage_table(tab, a.table);
-    if (active) stage_tile(tw, a.words, a.tile_off, t, lane, a.tile_lds_words);
+    // Everything the wave needs from memory before decoding is requested in
+    // one batch: initial states, stream offsets, the first block of x and
+    // step, the table and the tile block.
+    const int nk = a.C / nst;
+    const int colbase = cb * a.C + lane;
+    uint32_t st0[S], off0[S];
+    if (active) {
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            st0[s] = a.states[t * nst + 64 * s + lane];
+            off0[s] = a.soffs[t * nst + 64 * s + lane];
+        }
+    }
+    // x and step for KU column steps are loaded one block ahead of use, so
+    // their latency overlaps the decode of the current block.
+    constexpr int KU = 4;
+    uint32_t xr[KU][S][B];  // raw bits: bf16 zero-extended, or f32
+    float sr[KU][S];
+    auto load_block = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int k = k0 + u < nk ? k0 + u : nk - 1;
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                const int col = colbase + 64 * (S * k + s);
+                sr[u][s] = a.step[col];
+#pragma unroll
+                for (int b = 0; b < B; b++)
+                    xr[u][s][b] = load_x_bits(a.x, (int64_t)b * a.cols + col, XBF16);
+            }
+        }
+    };
+    if (active) load_block(0);
+    stage_table_and_tile(tab, a.table, raw, a.words, a.tile_off, t, active, lane, a.L.raw_words);
     if (threadIdx.x < R * B) esc_red[threadIdx.x] = 0.f;
     __syncthreads();
 
@@ -199,37 +292,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         for (int b = 0; b < B; b++) acc[r][b] = 0.f;
 
     if (active) {
-        uint32_t st[S], p[S], w[S];
-        const int sbase = t * 64 * S + lane;
-#pragma unroll
-        for (int s = 0; s < S; s++) {
-            st[s] = a.states[sbase + 64 * s];
-            p[s] = a.soffs[sbase + 64 * s];
-        }
-#pragma unroll
-        for (int s = 0; s < S; s++) w[s] = tw[p[s]];
-        const int nk = a.C / (64 * S);
-        const int colbase = cb * a.C + lane;
-        // x and step for KU column steps are loaded one block ahead of use,
-        // so their latency overlaps the decode of the current block.
-        constexpr int KU = 4;
-        uint32_t xr[KU][S][B];  // raw bits: bf16 zero-extended, or f32
-        float sr[KU][S];
-        auto load_block = [&](int k0) {
-#pragma unroll
-            for (int u = 0; u < KU; u++) {
-                const int k = k0 + u < nk ? k0 + u : nk - 1;
-#pragma unroll
-                for (int s = 0; s < S; s++) {
-                    const int col = colbase + 64 * (S * k + s);
-                    sr[u][s] = a.step[col];
-#pragma unroll
-                    for (int b = 0; b < B; b++)
-                        xr[u][s][b] = load_x_bits(a.x, (int64_t)b * a.cols + col, XBF16);
-                }
-            }
-        };
-        load_block(0);
+        Lanes<S> L;
+        init_lanes<S>(L, tab, raw, st0, off0);
         for (int k0 = 0; k0 < nk; k0 += KU) {
             float xv[KU][S][B];
 #pragma unroll
@@ -256,7 +320,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
                 for (int r = 0; r < R; r++) {
 #pragma unroll
                     for (int s = 0; s < S; s++) {
-                        const float code = (float)rans_step(st[s], p[s], w[s], tab, tw);
+                        const float code = (float)rans_step(L.st[s], L.a[s], L.w[s], L.e[s], tab);
 #pragma unroll
                         for (int b = 0; b < B; b++)
                             acc[r][b] = fmaf(code, xv[u][s][b], acc[r][b]);
@@ -348,7 +412,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     }
 }
 
-__device__ inline uint16_t f32_to_bf16_rne(float f) {
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     const uint32_t u = __float_as_uint(f);
     if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu))  // NaN stays NaN
         return (uint16_t)((u >> 16) | 0x40u);
@@ -359,31 +423,32 @@ __device__ inline uint16_t f32_to_bf16_rne(float f) {
 // One wave per tile; escapes are written afterwards by scatter_escapes.
 template <int R, int S, int MODE>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeArgs a) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    uint2* tab = reinterpret_cast<uint2*>(lds + kTabOff);
+    __shared__ __align__(16) uint2 tab[kProbM];
+    extern __shared__ __align__(16) uint16_t dyn[];
+    constexpr int nst = 64 * S;
     const int W = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar tile math
     const int lane = threadIdx.x & 63;
-    uint16_t* tw = reinterpret_cast<uint16_t*>(lds + kTileOff) + (size_t)wave * a.tile_lds_words;
+    uint16_t* raw = dyn + (size_t)wave * a.L.wave_words;
     const int t = blockIdx.x * W + wave;
     const bool active = t < a.ntiles;
 
-    stage_table(tab, a.table);
-    if (active) stage_tile(tw, a.words, a.tile_off, t, lane, a.tile_lds_words);
+    uint32_t st0[S], off0[S];
+    if (active) {
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            st0[s] = a.states[t * nst + 64 * s + lane];
+            off0[s] = a.soffs[t * nst + 64 * s + lane];
+        }
+    }
+    stage_table_and_tile(tab, a.table, raw, a.words, a.tile_off, t, active, lane, a.L.raw_words);
     __syncthreads();
     if (!active) return;
+    Lanes<S> L;
+    init_lanes<S>(L, tab, raw, st0, off0);
 
     const int rb = t / a.ncb, cb = t - rb * a.ncb;
-    uint32_t st[S], p[S], w[S];
-    const int sbase = t * 64 * S + lane;
-#pragma unroll
-    for (int s = 0; s < S; s++) {
-        st[s] = a.states[sbase + 64 * s];
-        p[s] = a.soffs[sbase + 64 * s];
-    }
-#pragma unroll
-    for (int s = 0; s < S; s++) w[s] = tw[p[s]];
-    const int nk = a.C / (64 * S);
+    const int nk = a.C / nst;
     const int colbase = cb * a.C + lane;
     for (int k = 0; k < nk; k++) {
         // Symbol order within a state is k-major, r-minor; the S states of a
@@ -393,7 +458,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
 #pragma unroll
             for (int s = 0; s < S; s++) {
                 const int col = colbase + 64 * (S * k + s);
-                const int32_t code = rans_step(st[s], p[s], w[s], tab, tw);
+                const int32_t code = rans_step(L.st[s], L.a[s], L.w[s], L.e[s], tab);
                 const int64_t o = ((int64_t)rb * R + r) * a.cols + col;
                 if (MODE == 0)
                     reinterpret_cast<int32_t*>(a.out)[o] = code;
@@ -452,14 +517,21 @@ __global__ void __launch_bounds__(256) int4_gemv_kernel(const uint32_t* __restri
 }
 
 // ------------------------------------------------------------------ host
-int tile_lds_words(const rans_w64_matrix* m) { return (m->max_tile_words + 7) & ~7; }
+WaveLayout wave_layout(const rans_w64_matrix* m) {
+    WaveLayout L;
+    L.raw_words = (m->max_tile_words + 8 + 7) & ~7;
+    L.wave_words = L.raw_words;
+    return L;
+}
 
-size_t lds_bytes(int waves, int tw_words) { return (size_t)kTileOff + (size_t)waves * tw_words * 2; }
+// Dynamic LDS bytes of a launch (the static arrays come on top).
+size_t lds_bytes(int waves, const WaveLayout& L) { return (size_t)waves * L.wave_words * 2; }
 
 bool valid_geometry(const rans_w64_matrix* m) {
     if (!m || m->rows <= 0 || m->cols <= 0 || m->R <= 0 || m->C <= 0 || m->S <= 0) return false;
     if (m->rows % m->R || m->cols % m->C || m->C % (64 * m->S)) return false;
     if (m->max_tile_words <= 0 || m->max_tile_words > 65536) return false;
+    if (m->max_state_words <= 0 || m->max_state_words > m->max_tile_words) return false;
     return true;
 }
 
@@ -472,16 +544,16 @@ bool valid_pointers(const rans_w64_matrix* m) {
 // LDS footprint fits.  Returns 0 when even one wave does not fit.
 int gemv_waves(const rans_w64_matrix* m) {
     const int ncb = m->cols / m->C;
-    const int tw = tile_lds_words(m);
+    const WaveLayout L = wave_layout(m);
     for (int w = kMaxWaves; w >= 1; w--)
-        if (ncb % w == 0 && lds_bytes(w, tw) <= (size_t)kLdsMax) return w;
+        if (ncb % w == 0 && lds_bytes(w, L) + kStaticLds <= (size_t)kLdsMax) return w;
     return 0;
 }
 
 int decode_waves(const rans_w64_matrix* m) {
-    const int tw = tile_lds_words(m);
+    const WaveLayout L = wave_layout(m);
     for (int w = 4; w >= 1; w >>= 1)
-        if (lds_bytes(w, tw) <= (size_t)kLdsMax) return w;
+        if (lds_bytes(w, L) + kStaticLds <= (size_t)kLdsMax) return w;
     return 0;
 }
 
@@ -495,11 +567,12 @@ const void* g_attr_done[512];
 int g_attr_n = 0;
 
 hipError_t ensure_lds(const void* fn, size_t bytes) {
-    if (bytes <= 65536) return hipSuccess;
+    if (bytes + kStaticLds <= 65536) return hipSuccess;
     std::lock_guard<std::mutex> lk(g_attr_mu);
     for (int i = 0; i < g_attr_n; i++)
         if (g_attr_done[i] == fn) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       kLdsMax - kStaticLds);
     if (e == hipSuccess && g_attr_n < 512) g_attr_done[g_attr_n++] = fn;
     return e;
 }
@@ -599,10 +672,9 @@ int launch_decode_common(const rans_w64_matrix* m, void* out, hipStream_t stream
     a.C = m->C;
     a.ncb = m->cols / m->C;
     a.ntiles = (m->rows / m->R) * a.ncb;
-    a.tile_lds_words = tile_lds_words(m);
+    a.L = wave_layout(m);
     const int grid = (a.ntiles + waves - 1) / waves;
-    int rc = dispatch_decode<MODE>(a, m->R, m->S, waves, lds_bytes(waves, a.tile_lds_words), grid,
-                                   stream);
+    int rc = dispatch_decode<MODE>(a, m->R, m->S, waves, lds_bytes(waves, a.L), grid, stream);
     if (rc != 0) return rc;
     hipLaunchKernelGGL((scatter_escapes_kernel<MODE>), dim3((m->rows + 255) / 256), dim3(256), 0,
                        stream, m->esc_rowptr, m->esc_col, m->esc_val, m->step, out, m->rows,
@@ -652,12 +724,12 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
     a.C = m->C;
     a.ncb = ncb;
     a.ngroups = ngroups;
-    a.tile_lds_words = tile_lds_words(m);
+    a.L = wave_layout(m);
     a.counters = ngroups > 1 ? static_cast<uint32_t*>(m->workspace) : nullptr;
     a.partial = ngroups > 1
                     ? reinterpret_cast<float*>(static_cast<uint8_t*>(m->workspace) + counters_bytes(m))
                     : nullptr;
-    const size_t lds = lds_bytes(waves, a.tile_lds_words);
+    const size_t lds = lds_bytes(waves, a.L);
     const int grid = (m->rows / m->R) * ngroups;
 
     // Batches run in chunks of 4 vectors, the remainder one vector at a time.

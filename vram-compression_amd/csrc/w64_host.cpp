@@ -30,6 +30,7 @@ struct Encoded {
     std::vector<int32_t> esc_rowptr, esc_col, esc_val;
     int64_t payload_words = 0;
     int32_t max_tile_words = 0;
+    int32_t max_state_words = 0;  // longest state stream, counting the tile padding
 };
 
 // Runs fn(i) for i in [0, n) on up to nthreads threads, static blocks.
@@ -136,6 +137,7 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
     E->states.assign((size_t)(ntiles * nst), 0);
     std::vector<int64_t> payload((size_t)ntiles, 0);
     std::vector<int> too_big((size_t)ntiles, 0);
+    std::vector<int32_t> longest((size_t)ntiles, 0);
 
     const int64_t* freq = E->freq;
     parallel_for(ntiles, nthreads > 0 ? nthreads : 1, [&](int64_t t) {
@@ -177,6 +179,15 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
         const size_t padded = (blk.size() + 1 + 7) & ~(size_t)7;
         if (padded > 65535) too_big[(size_t)t] = 1;
         blk.resize(padded, 0);
+        // stream lengths as the decoder stages them: up to the next state's
+        // start, the last one up to the end of the padded block
+        int32_t lmax = 0;
+        for (int32_t j = 0; j < nst; j++) {
+            const size_t sid = (size_t)(t * nst + j);
+            const int64_t end = j + 1 < nst ? E->soffs[sid + 1] : (int64_t)padded;
+            lmax = std::max<int32_t>(lmax, (int32_t)(end - E->soffs[sid]));
+        }
+        longest[(size_t)t] = lmax;
     });
     for (int64_t t = 0; t < ntiles; t++) {
         if (too_big[(size_t)t]) {
@@ -191,6 +202,7 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
         E->tile_off[(size_t)t] = (uint32_t)total;
         total += (int64_t)blocks[(size_t)t].size();
         E->max_tile_words = std::max<int32_t>(E->max_tile_words, (int32_t)blocks[(size_t)t].size());
+        E->max_state_words = std::max<int32_t>(E->max_state_words, longest[(size_t)t]);
         E->payload_words += payload[(size_t)t];
     }
     if (total > 0xFFFFFFFFll) {
@@ -210,6 +222,7 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
     info[3] = (int64_t)E->esc_col.size();
     info[4] = E->max_tile_words;
     info[5] = E->payload_words;
+    info[6] = E->max_state_words;
     *handle = E;
     return 0;
 }

@@ -45,7 +45,8 @@ class RansMatrixDesc(ctypes.Structure):
     """ctypes mirror of rans_w64_matrix (include/vramc_rans.h)."""
     _fields_ = [("rows", ctypes.c_int32), ("cols", ctypes.c_int32),
                 ("R", ctypes.c_int32), ("C", ctypes.c_int32), ("S", ctypes.c_int32),
-                ("max_tile_words", ctypes.c_int32),
+                ("max_tile_words", ctypes.c_int32), ("max_state_words", ctypes.c_int32),
+                ("reserved", ctypes.c_int32),
                 ("words", ctypes.c_void_p), ("tile_off", ctypes.c_void_p),
                 ("soffs", ctypes.c_void_p), ("states", ctypes.c_void_p),
                 ("table", ctypes.c_void_p), ("esc_rowptr", ctypes.c_void_p),
@@ -163,13 +164,14 @@ def encode(codes, R, C, S=1, threads=None):
         "shape not divisible into R x C tiles with C % (64*S) == 0"
     lib = _host_lib()
     h = ctypes.c_void_p()
-    info = np.zeros(6, np.int64)
+    info = np.zeros(7, np.int64)
     nthreads = threads or min(16, os.cpu_count() or 1)
     rc = lib.rans_w64_encode(_p(codes), rows, cols, R, C, S, nthreads, ctypes.byref(h), _p(info))
     assert rc != -5, "degenerate distribution (single symbol)"
     assert rc != -6, "a tile needs more than 65535 words: use smaller R or C"
     assert rc == 0, f"encode failed ({rc})"
-    nwords, ntiles, nstates, nesc, max_tile_words, payload_words = (int(v) for v in info)
+    nwords, ntiles, nstates, nesc, max_tile_words, payload_words, max_state_words = \
+        (int(v) for v in info)
     words = np.zeros(nwords, np.uint16)
     tile_off = np.zeros(ntiles + 1, np.uint32)
     soffs = np.zeros(nstates, np.uint16)
@@ -193,6 +195,7 @@ def encode(codes, R, C, S=1, threads=None):
     return dict(words=words, tile_off=tile_off, soffs=soffs, states=states, table=table,
                 esc_rowptr=esc_rowptr, esc_col=esc_col, esc_val=esc_val,
                 R=R, C=C, S=S, shape=codes.shape, max_tile_words=max_tile_words,
+                max_state_words=max_state_words,
                 bits_payload=16 * payload_words / N,
                 bits_state_offs=(48 * nstates + 32 * (ntiles + 1) + 16 * pad_words) / N,
                 bits_table=32 * M / N,
@@ -207,7 +210,8 @@ def _host_desc(enc, keep):
     keep.append(arrs)
     rows, cols = enc["shape"]
     d = RansMatrixDesc(rows=rows, cols=cols, R=enc["R"], C=enc["C"], S=enc["S"],
-                       max_tile_words=enc["max_tile_words"])
+                       max_tile_words=enc["max_tile_words"],
+                       max_state_words=enc["max_state_words"])
     for k, a in arrs.items():
         setattr(d, k, a.ctypes.data if a.size else None)
     return d
@@ -261,9 +265,10 @@ class RansMatrix:
         assert step.numel() == self.cols, "step must have one value per column"
         self.step = step.float().reshape(self.cols).contiguous().to(dev)
         self.max_tile_words = int(enc["max_tile_words"])
+        self.max_state_words = int(enc["max_state_words"])
         self._desc = RansMatrixDesc(
             rows=self.rows, cols=self.cols, R=self.R, C=self.C, S=self.S,
-            max_tile_words=self.max_tile_words,
+            max_tile_words=self.max_tile_words, max_state_words=self.max_state_words,
             words=self.words.data_ptr(), tile_off=self.tile_off.data_ptr(),
             soffs=self.soffs.data_ptr(), states=self.states.data_ptr(),
             table=self.table.data_ptr(), esc_rowptr=self.esc_rowptr.data_ptr(),
