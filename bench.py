@@ -211,7 +211,22 @@ def main():
         rocblas = {"us_per_gemv": tb_rot, "effective_GBps": ROWS * COLS * 2 / tb_rot / 1e3,
                    "hot_us_per_gemv": tb_hot, "copies": nW,
                    "speedup_rans_vs_bf16": tb_rot / t_rot}
-        del Ws
+        del Ws, fns
+        # the reference's other comparators (kernel/bench.py:97-111): the
+        # fixed-rate int4 GEMV (host fold + int4 kernel) and decode-to-bf16
+        # followed by the bf16 GEMV
+        m4s = [rans.Int4Matrix(np.clip(codes, -8, 7), step_t, lib)
+               for _ in range(max(2, -(-ROTATE_BYTES // (ROWS * COLS // 2))))]
+        xf = xb.float()
+        y4 = torch.empty(ROWS, device="cuda")
+        rocblas["int4_us_per_gemv"] = graph_time_us([lambda m4=m4: m4.gemv(xf, y4) for m4 in m4s],
+                                                    args.steps, args.warmup)
+        del m4s
+        m = rans.RansMatrix(enc, step_t, lib)
+        buf = torch.empty(ROWS, COLS, device="cuda", dtype=torch.bfloat16)
+        rocblas["decode_then_bf16_us_per_gemv"] = graph_time_us(
+            [lambda: torch.nn.functional.linear(xb, m.decode(buf))], 50, args.warmup)
+        del m, buf
         torch.cuda.empty_cache()
         print(f"bf16 F.linear: {tb_rot:.2f} us rotated, {tb_hot:.2f} us hot", file=sys.stderr,
               flush=True)

@@ -16,8 +16,8 @@ for p in (PKG, ORACLE):
 
 
 def pytest_collection_modifyitems(config, items):
-    # The six largest published records (34816x5120, 5120x17408) take about
-    # three minutes of CPU; they run when RUN_SLOW=1.
+    # The published records larger than the 1536x8960 metric shape take
+    # several minutes of CPU; they run when RUN_SLOW=1.
     if os.environ.get("RUN_SLOW") == "1":
         return
     skip = pytest.mark.skip(reason="slow CPU case; set RUN_SLOW=1")

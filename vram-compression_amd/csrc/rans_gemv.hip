@@ -10,10 +10,9 @@
 //   2. each wavefront copies its tile's compressed block into LDS with
 //      16-byte loads (coalesced across the 64 lanes), issued together with
 //      the table loads so both latencies overlap;
-//   3. inside LDS each lane re-lays its states' word streams column-wise
-//      (word i of state j at row i, column j): the data-dependent
-//      renormalisation reads of the 64 lanes then fall into a few adjacent
-//      rows (at most 2-way bank conflicts) instead of 64 random addresses;
+//   3. each state reads its renormalisation words straight from the staged
+//      block at its own offset (a per-state LDS byte address that advances
+//      by 2 on each refill);
 //   4. each lane runs S independent rANS states; per column step a lane
 //      loads x[c]*step[c] once (the waterfilling fold happens here, one block
 //      of column steps ahead of use) and reuses it for the R rows of the tile;
@@ -37,10 +36,24 @@ constexpr uint32_t kRansL = 1u << 16;
 constexpr int kMaxWaves = 8;
 constexpr int kMaxRB = 64;  // largest R*B compiled (16 * 4)
 
+// Table entry layout in LDS.  8 bytes (default): {freq | code<<24, bias},
+// one mad consumes both words and the code is the top byte.  4 bytes
+// (VRAMC_TABLE32=1): code | freq<<8 | bias<<20, one bit-field extract and
+// one shift more per symbol but half the LDS bank traffic of the lookup.
+#ifndef VRAMC_TABLE32
+#define VRAMC_TABLE32 0
+#endif
+#if VRAMC_TABLE32
+using TabEntry = uint32_t;
+#else
+using TabEntry = uint2;
+#endif
+
 // LDS: the expanded table and the reduction scratch are static __shared__
 // arrays (their offsets are compile-time constants, so table addressing
 // needs no base add); the per-wave regions are dynamic.
-constexpr int kStaticLds = 8 * (int)kProbM + 4 * kMaxWaves * kMaxRB + 4 * kMaxRB + 16;
+constexpr int kStaticLds =
+    (int)sizeof(TabEntry) * (int)kProbM + 4 * kMaxWaves * kMaxRB + 4 * kMaxRB + 16;
 constexpr int kLdsMax = 160 * 1024;
 
 // 32-bit LDS addresses (address space 3), so a word read is one ds_read with
@@ -90,13 +103,35 @@ struct DecodeArgs {
     WaveLayout L;
 };
 
-// Reference-packed table entry (sym | freq<<8 | bias<<20) -> LDS pair
-// {freq | code<<24, bias}; the escape symbol (0) gets code 0 so it adds
-// nothing in the GEMV and is patched from the side table.
-__device__ __forceinline__ uint2 expand_entry(uint32_t e) {
+// Reference-packed table entry (sym | freq<<8 | bias<<20) -> LDS entry;
+// the escape symbol (0) gets code 0 so it adds nothing in the GEMV and is
+// patched from the side table.
+__device__ __forceinline__ TabEntry expand_entry(uint32_t e) {
     const uint32_t sym = e & 0xFFu;
     const uint32_t code = sym == 0 ? 0u : (uint32_t)((int32_t)sym - 128);
+#if VRAMC_TABLE32
+    return (e & ~0xFFu) | (code & 0xFFu);
+#else
     return make_uint2(((e >> 8) & 0xFFFu) | (code << 24), e >> 20);
+#endif
+}
+
+// freq*(st>>12) + bias (rans_gemv.cu:34): freq < 2^12 and st>>12 < 2^20
+// both fit the 24-bit multiplier.
+__device__ __forceinline__ uint32_t entry_next_state(TabEntry e, uint32_t st) {
+#if VRAMC_TABLE32
+    return __umul24((e >> 8) & 0xFFFu, st >> 12) + (e >> 20);
+#else
+    return __umul24(e.x, st >> 12) + e.y;
+#endif
+}
+
+__device__ __forceinline__ int32_t entry_code(TabEntry e) {
+#if VRAMC_TABLE32
+    return (int32_t)(int8_t)(e & 0xFFu);
+#else
+    return (int32_t)e.x >> 24;
+#endif
 }
 
 // Keeps the four registers of v live here: the loads that produce them
@@ -111,7 +146,7 @@ __device__ __forceinline__ void pin(const uint4& v) {
 // first LDS write, so the workgroup pays one memory latency.  Loads use
 // clamped indices (unconditional: a guarded load becomes a branch with its
 // own wait); stores are guarded, so no two lanes store to one address.
-__device__ __forceinline__ void stage_table_and_tile(uint2* tab, const uint32_t* __restrict__ table,
+__device__ __forceinline__ void stage_table_and_tile(TabEntry* tab, const uint32_t* __restrict__ table,
                                                      uint16_t* raw,
                                                      const uint16_t* __restrict__ words,
                                                      const uint32_t* __restrict__ tile_off, int t,
@@ -194,13 +229,13 @@ struct Lanes {
     uint32_t st[S];  // rANS states
     uint32_t a[S];   // LDS byte address of the next unread word of each state
     uint32_t w[S];   // that word (read ahead)
-    uint2 e[S];      // table entry for the next symbol of each state
+    TabEntry e[S];   // table entry for the next symbol of each state
 };
 
 // Staged-block setup: each state's read pointer, its first word and the
 // table entry of its first symbol.  Call after the staging barrier.
 template <int S>
-__device__ __forceinline__ void init_lanes(Lanes<S>& L, const uint2* tab, const uint16_t* raw,
+__device__ __forceinline__ void init_lanes(Lanes<S>& L, const TabEntry* tab, const uint16_t* raw,
                                            const uint32_t (&st0)[S], const uint32_t (&off0)[S]) {
 #pragma unroll
     for (int s = 0; s < S; s++) {
@@ -217,21 +252,21 @@ __device__ __forceinline__ void init_lanes(Lanes<S>& L, const uint2* tab, const 
 // entry for the following symbol is read as soon as the new state exists,
 // before the code conversion and the word-pointer update, so those overlap
 // the LDS latency instead of sitting on the state's dependency chain.
-__device__ __forceinline__ int32_t rans_step(uint32_t& st, uint32_t& a, uint32_t& w, uint2& e,
-                                             const uint2* tab) {
-    const uint2 cur = e;
-    const uint32_t ns = __umul24(cur.x, st >> 12) + cur.y;  // freq < 2^12, st>>12 < 2^20
+__device__ __forceinline__ int32_t rans_step(uint32_t& st, uint32_t& a, uint32_t& w, TabEntry& e,
+                                             const TabEntry* tab) {
+    const TabEntry cur = e;
+    const uint32_t ns = entry_next_state(cur, st);
     const bool need = ns < kRansL;
     st = need ? ((ns << 16) | w) : ns;
     e = tab[st & (kProbM - 1)];
     a += need ? 2u : 0u;
     w = lds_read_u16(a);
-    return (int32_t)cur.x >> 24;
+    return entry_code(cur);
 }
 
 template <int R, int S, int B, bool XBF16>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs a) {
-    __shared__ __align__(16) uint2 tab[kProbM];
+    __shared__ __align__(16) TabEntry tab[kProbM];
     __shared__ float red[kMaxWaves * kMaxRB];
     __shared__ float esc_red[kMaxRB];
     __shared__ int flag[4];
@@ -423,7 +458,7 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 // One wave per tile; escapes are written afterwards by scatter_escapes.
 template <int R, int S, int MODE>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeArgs a) {
-    __shared__ __align__(16) uint2 tab[kProbM];
+    __shared__ __align__(16) TabEntry tab[kProbM];
     extern __shared__ __align__(16) uint16_t dyn[];
     constexpr int nst = 64 * S;
     const int W = blockDim.x >> 6;

@@ -21,6 +21,7 @@ import torch
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 import rans  # noqa: E402
+from rans import encode  # noqa: E402
 
 RES = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "results")
 
@@ -73,7 +74,8 @@ def synth_codes_full(rows, cols, target_bits, dist="laplace", seed=0, escape_fra
     FULL tensor's empirical entropy is target_bits +- tol (no clipping: the
     levels are unbounded).  The bisection runs on a 2^22-element sample and is
     refined on the full tensor.  escape_frac of the positions (chosen at
-    random) are then forced to |code| in [128, 600), beyond the table range."""
+    random, each independently) are then forced to |code| in [128, 600),
+    beyond the table range."""
     rng = np.random.default_rng(seed)
     w = _weights(rng, (rows, cols), dist)
     flat = w.ravel()
@@ -96,8 +98,8 @@ def synth_codes_full(rows, cols, target_bits, dist="laplace", seed=0, escape_fra
         codes = np.round(w / np.exp(logd)).astype(np.int64)
     codes = codes.astype(np.int32)
     if escape_frac > 0:
-        n = max(1, int(round(escape_frac * codes.size)))
-        pos = rng.choice(codes.size, n, replace=False)
+        pos = np.flatnonzero(rng.random(codes.size) < escape_frac)
+        n = pos.size
         mag = rng.integers(128, 600, n)
         sign = np.where(rng.random(n) < 0.5, -1, 1)
         codes.ravel()[pos] = (sign * mag).astype(np.int32)
@@ -160,18 +162,27 @@ def timeit_graph(fns, iters=200, warmup=10):
 # ---------------------------------------------------------------- harness
 def pick_tiling(rows, cols, R=None, S=1, target_states=None):
     """A legal (R, C) for the w64 format: C a multiple of 64*S dividing cols,
-    chosen so about `target_states` states cover the matrix (fewer states
-    mean less per-state overhead, more mean more parallelism)."""
+    R in {1, 2, 4, 8, 16}, chosen so about `target_states` states cover the
+    matrix (fewer states mean less per-state overhead, more mean more
+    parallelism).  Tilings whose 4..8 column tiles fill one workgroup are
+    preferred: fewer waves per workgroup repeat the table staging more often,
+    more column tiles than 8 need the split-K reduction."""
     nst = 64 * S
     cands = [c for c in range(nst, cols + 1, nst) if cols % c == 0]
     assert cands, f"cols={cols} has no divisor that is a multiple of {nst}"
     Rs = [R] if R else [r for r in (16, 8, 4, 2, 1) if rows % r == 0]
-    target = target_states or 98304
+    # about 140 symbols per state; small matrices get more states (down to
+    # 64 symbols each) so the chip has about one wavefront per SIMD, large
+    # ones stop at what saturates it (about 3 per SIMD)
+    n = rows * cols
+    target = target_states or int(min(max(n // 140, min(98304, n // 64)), 262144))
     best = None
     for r in Rs:
         for c in cands:
             states = (rows // r) * (cols // c) * nst
-            key = (abs(np.log(states / target)), -c)
+            ncb = cols // c
+            penalty = 0.0 if 4 <= ncb <= 8 else (0.35 if ncb < 4 else 0.5)
+            key = (abs(np.log(states / target)) + penalty, -c)
             if best is None or key < best[0]:
                 best = (key, r, c)
     return best[1], best[2]
@@ -263,5 +274,134 @@ def bench(rotate_bytes=512 << 20, iters=200):
         json.dump(out, f, indent=1)
 
 
+# ------------------------------------------------ benchmark configurations
+def qwen15b_layer_shapes():
+    """(name, rows, cols) of one Qwen2.5-1.5B decoder layer's linear maps."""
+    return [("q", 1536, 1536), ("k", 256, 1536), ("v", 256, 1536), ("o", 1536, 1536),
+            ("gate", 8960, 1536), ("up", 8960, 1536), ("down", 1536, 8960)]
+
+
+def chain_tiling(rows, cols):
+    """Tiling for one matrix of the per-token chain: about 140 symbols per
+    state on large matrices, fewer on small ones (whose decode would
+    otherwise be latency-bound far above their byte count)."""
+    n = rows * cols
+    target = max(n // 140, min(n // 35, 49152))
+    return pick_tiling(rows, cols, S=1, target_states=target)
+
+
+def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None, C=None, S=1,
+                  iters=100, rotate_bytes=512 << 20):
+    """Times one encoded matrix (rotated over >= rotate_bytes of copies) and
+    the bf16 F.linear on the same shape and rotation; checks the GEMV."""
+    codes = synth_codes_full(rows, cols, bits, dist=dist, seed=seed, escape_frac=escape_frac)
+    step = torch.from_numpy(lognormal_steps(cols, seed=seed))
+    if R is None or C is None:
+        R, C = pick_tiling(rows, cols, S=S)
+    enc = encode(codes, R, C, S)
+    m = rans.RansMatrix(enc, step, lib)
+    ncopy = max(2, -(-rotate_bytes // m.nbytes))
+    ms = [m] + [rans.RansMatrix(enc, step, lib) for _ in range(ncopy - 1)]
+    x = torch.randn(batch, cols, device="cuda").bfloat16()
+    y = torch.empty(batch, rows, device="cuda")
+    t_rans = timeit_graph([lambda mm=mm: mm.gemv(x, y) for mm in ms], iters)
+    nW = max(2, -(-rotate_bytes // (rows * cols * 2)))
+    W = (torch.from_numpy(codes.astype(np.float32)) * step).bfloat16().cuda()
+    Ws = [W] + [W.clone() for _ in range(nW - 1)]
+    t_bf16 = timeit_graph([lambda Wd=Wd: torch.nn.functional.linear(x, Wd) for Wd in Ws], iters)
+    ref = torch.nn.functional.linear(x.float(), W.float())
+    got = ms[0].gemv(x)
+    err = float((got - ref).norm() / ref.norm())
+    out = dict(rows=rows, cols=cols, bits_target=bits, dist=dist, escape_frac=escape_frac,
+               batch=batch, R=R, C=C, S=S, entropy=entropy_fast(codes),
+               bits_total=8 * m.nbytes / codes.size, n_escapes=int(len(enc["esc_col"])),
+               t_rans_us=t_rans, t_bf16_us=t_bf16,
+               effective_GBps=rows * cols * 2 / t_rans / 1e3,
+               compressed_GBps=m.nbytes / t_rans / 1e3,
+               speedup_vs_bf16=t_bf16 / t_rans, rel_l2_vs_bf16_fp32=err, copies=ncopy)
+    del ms, Ws
+    torch.cuda.empty_cache()
+    return out
+
+
+def chain(bits=3.25, layers=28, seed=0, iters=3):
+    """Per-token chain of 7*layers batch-1 GEMVs over a random-init
+    Qwen2.5-1.5B-shaped weight set (one table per matrix, ECSQ-like Laplace
+    codes at `bits` bits/weight), graph-captured and replayed; the same chain
+    with bf16 F.linear.  Returns the total weight-pass latency of both."""
+    lib = rans.build()
+    rng = np.random.default_rng(seed)
+    mats, Ws, xs = [], [], {}
+    nbytes = 0
+    nweights = 0
+    # one step per shape, chosen on a sample, so every layer has ~`bits` bits
+    deltas = {}
+    for name, rows, cols in qwen15b_layer_shapes():
+        sample = rng.laplace(size=1 << 20)
+        lo, hi = -12.0, 6.0
+        for _ in range(40):
+            mid = (lo + hi) / 2
+            h = entropy_fast(np.round(sample / np.exp(mid)).astype(np.int64))
+            lo, hi = (mid, hi) if h > bits else (lo, mid)
+        deltas[name] = np.exp((lo + hi) / 2)
+    for layer in range(layers):
+        for name, rows, cols in qwen15b_layer_shapes():
+            codes = np.round(rng.laplace(size=(rows, cols)) / deltas[name]).astype(np.int32)
+            step = torch.from_numpy(lognormal_steps(cols, seed=seed + layer))
+            R, C = chain_tiling(rows, cols)
+            enc = encode(codes, R, C, 1)
+            m = rans.RansMatrix(enc, step, lib)
+            mats.append(m)
+            nbytes += m.nbytes
+            nweights += codes.size
+            Ws.append((torch.from_numpy(codes.astype(np.float32)) * step).bfloat16().cuda())
+            if cols not in xs:
+                xs[cols] = torch.randn(cols, device="cuda").bfloat16()
+            print(f"chain: layer {layer} {name} encoded", file=sys.stderr, flush=True) \
+                if name == "down" and layer % 7 == 0 else None
+    ys = {r: torch.empty(r, device="cuda") for r in {m.rows for m in mats}}
+
+    def run_rans():
+        for m in mats:
+            m.gemv(xs[m.cols], ys[m.rows])
+
+    def run_bf16():
+        for W in Ws:
+            torch.nn.functional.linear(xs[W.shape[1]], W)
+
+    t_rans = timeit_graph(run_rans, iters, warmup=2)
+    t_bf16 = timeit_graph(run_bf16, iters, warmup=2)
+    return dict(config="Qwen2.5-1.5B-shaped weight set, 28 layers x 7 matrices, batch 1",
+                gemvs=len(mats), weights=nweights, bits_target=bits,
+                bits_total=8 * nbytes / nweights, compressed_MB=nbytes / 1e6,
+                bf16_MB=nweights * 2 / 1e6, t_rans_us=t_rans, t_bf16_us=t_bf16,
+                effective_GBps=nweights * 2 / t_rans / 1e3, speedup_vs_bf16=t_bf16 / t_rans)
+
+
+def configs():
+    """The benchmark configurations beyond the headline shape: MLP shapes at
+    2.25 bits with 0.1% escapes, q_proj at 4.25 bits, the 27B-class shapes
+    with Student-t codes and 1% escapes at batch 1 and 4, and the per-token
+    196-GEMV chain.  Prints one JSON line per result."""
+    lib = rans.build()
+    cases = [
+        ("q_proj 4.25b gauss", 1536, 1536, 4.25, "gauss", 0.0, 1),
+        ("gate/up 2.25b esc0.1%", 8960, 1536, 2.25, "laplace", 0.001, 1),
+        ("down 2.25b esc0.1%", 1536, 8960, 2.25, "laplace", 0.001, 1),
+        ("27B 25600x5120 t3 2.25b esc1% B1", 25600, 5120, 2.25, "student3", 0.01, 1),
+        ("27B 25600x5120 t3 2.25b esc1% B4", 25600, 5120, 2.25, "student3", 0.01, 4),
+        ("27B 5120x25600 t3 2.25b esc1% B1", 5120, 25600, 2.25, "student3", 0.01, 1),
+        ("27B 5120x25600 t3 2.25b esc1% B4", 5120, 25600, 2.25, "student3", 0.01, 4),
+    ]
+    for name, rows, cols, bits, dist, esc, batch in cases:
+        r = config_matrix(rows, cols, bits, dist, esc, batch, seed=rows + cols, lib=lib)
+        r["case"] = name
+        print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}),
+              flush=True)
+    r = chain()
+    print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}),
+          flush=True)
+
+
 if __name__ == "__main__":
-    {"test": test, "bench": bench}[sys.argv[1]]()
+    {"test": test, "bench": bench, "configs": configs}[sys.argv[1]]()
