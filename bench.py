@@ -44,12 +44,12 @@ DEFAULT_TILING = (4, 2240, 1)
 
 
 def algorithmic_bytes(enc, rows, cols, batch=1):
-    """Bytes one GEMV must move: the whole compressed matrix (payload and
-    padding words, tile offsets, per-state offsets and initial states, the
-    16 KB table, the escape side table), x (bf16), the step vector (f32) and
-    y (f32)."""
+    """Bytes one GEMV must move: the whole compressed matrix as the device
+    holds it (payload and padding words, tile offsets, per-state offsets and
+    initial states, the 32 KB LDS image of the table, the escape side table),
+    x (bf16), the step vector (f32) and y (f32)."""
     comp = (enc["words"].nbytes + enc["tile_off"].nbytes + enc["soffs"].nbytes +
-            enc["states"].nbytes + enc["table"].nbytes + enc["esc_rowptr"].nbytes +
+            enc["states"].nbytes + 2 * enc["table"].nbytes + enc["esc_rowptr"].nbytes +
             enc["esc_col"].nbytes + enc["esc_val"].nbytes)
     return comp, comp + cols * 2 * batch + cols * 4 + rows * 4 * batch
 

@@ -73,7 +73,9 @@ typedef struct rans_w64_matrix {
     const uint32_t* tile_off; /* [ntiles+1], in words, multiples of 8 */
     const uint16_t* soffs;    /* [ntiles*64*S] */
     const uint32_t* states;   /* [ntiles*64*S] */
-    const uint32_t* table;    /* [4096], reference packing */
+    const uint32_t* table;    /* [4096], reference packing (host decoder) */
+    const uint32_t* table_lds;/* [8192], the table as the kernels hold it in LDS, made
+                                 by rans_table_lds from table (device kernels) */
     const int32_t* esc_rowptr;/* [rows+1] */
     const int32_t* esc_col;   /* [nesc] */
     const int32_t* esc_val;   /* [nesc] */
@@ -119,6 +121,14 @@ int launch_int4_gemv(const void* w, const void* x, void* y, int rows, int cols,
  * distribution. */
 int rans_build_table(const uint8_t* sym, int64_t n, int64_t* freq, int64_t* cum,
                      uint32_t* table);
+
+/* The LDS image of a reference-packed table: out[2*slot] = freq | code<<24
+ * (code = sym-128, and 0 for the escape symbol 0, whose value comes from the
+ * side table), out[2*slot+1] = slot - cum.  The device kernels copy these
+ * 32 KB into LDS verbatim.  No reference counterpart: the reference unpacks
+ * the fields on every symbol (rans_gemv.cu:33-36).  Returns RANS_EARG for a
+ * null pointer. */
+int rans_table_lds(const uint32_t* table, uint32_t* out);
 
 /* Encode int32 codes (rows x cols, row-major) into the w64 format; replaces
  * encode() (rans.py:62-98).  On success *handle owns the result and info[]

@@ -34,6 +34,7 @@ def _desc(rans, rows=256, cols=4096, R=8, C=256, S=1, mtw=1024):
     return rans.RansMatrixDesc(rows=rows, cols=cols, R=R, C=C, S=S, max_tile_words=mtw,
                                max_state_words=64,
                                words=fake, tile_off=fake, soffs=fake, states=fake, table=fake,
+                               table_lds=fake,
                                esc_rowptr=fake, esc_col=fake, esc_val=fake, step=fake,
                                workspace=None, workspace_bytes=0)
 
@@ -58,6 +59,11 @@ def test_argument_validation_without_gpu(rans, lib):
     assert lib.rans_gemv_workspace_bytes(ctypes.byref(one), 1) == 0
     huge = _desc(rans, mtw=70000)
     assert lib.rans_gemv_workspace_bytes(ctypes.byref(huge), 1) == -2
+    no_img = _desc(rans)
+    no_img.table_lds = None  # the kernels need the table's LDS image
+    assert lib.launch_rans_gemv(ctypes.byref(no_img), x, 0, 1, y, None) == -4
+    assert lib.launch_rans_decode_codes(ctypes.byref(no_img), y, None) == -4
+    assert lib.rans_table_lds(None, y) == -4
     assert lib.launch_rans_decode(None, y, None) == -2
     assert lib.launch_rans_decode_codes(ctypes.byref(d), None, None) == -4
     assert lib.launch_int4_gemv(None, x, y, 4, 64, None) == -4

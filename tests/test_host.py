@@ -128,6 +128,26 @@ def test_build_table_matches_oracle(rans, oracle, golden):
             np.testing.assert_array_equal(a, b)
 
 
+def test_table_lds_image(rans, oracle, golden):
+    """The LDS image the kernels copy verbatim: per slot of symbol y,
+    {freq[y] | code<<24, slot - cum[y]} with code = y-128 (0 for the escape
+    symbol), rebuilt here from freq/cum rather than from the packed table."""
+    for name in ["two_symbols", "tie_argmax", "laplace"]:
+        sym = golden[f"tab_{name}_sym"]
+        freq, cum, table = oracle.build_table(sym)
+        img = rans.table_lds(table)
+        assert img.dtype == np.uint32 and img.size == 8192
+        for y in np.nonzero(freq)[0]:
+            code = 0 if y == 0 else int(y) - 128
+            slots = np.arange(cum[y], cum[y] + freq[y])
+            np.testing.assert_array_equal(img[2 * slots], np.uint32(freq[y] | ((code & 0xFF) << 24)))
+            np.testing.assert_array_equal(img[2 * slots + 1], (slots - cum[y]).astype(np.uint32))
+    esc = np.zeros(4096, np.uint32)  # every slot the escape symbol 0 with freq 4096-like fields
+    esc[:] = 0 | (5 << 8) | (3 << 20)
+    img = rans.table_lds(esc)
+    assert np.all(img[0::2] == 5) and np.all(img[1::2] == 3)
+
+
 def test_lane_order_matches_oracle(rans, oracle):
     a = np.arange(32 * 1024).reshape(32, 1024)
     for R, C, S in [(1, 64, 1), (4, 256, 2), (8, 1024, 4), (32, 512, 1)]:

@@ -3,13 +3,14 @@
 // documented in include/vramc_rans.h.
 //
 // Kernel shape (one workgroup = W wavefronts = W tiles of one tile row):
-//   1. the 4096-slot symbol table is expanded into LDS as {freq | code<<24,
-//      slot-cum} pairs, so one ds_read_b64 yields both rANS operands and the
-//      signed code (the reference keeps sym|freq<<8|bias<<20 and extracts the
-//      fields with three more ALU ops per symbol, rans_gemv.cu:33-36);
-//   2. each wavefront copies its tile's compressed block into LDS with
-//      16-byte loads (coalesced across the 64 lanes), issued together with
-//      the table loads so both latencies overlap;
+//   1. the 4096-slot symbol table sits in LDS as {freq | code<<24, slot-cum}
+//      pairs, so one ds_read_b64 yields both rANS operands and the signed
+//      code (the reference keeps sym|freq<<8|bias<<20 and extracts the
+//      fields with three more ALU ops per symbol, rans_gemv.cu:33-36).  That
+//      32 KB image is built once on the host (rans_table_lds) and copied
+//      into LDS with direct global->LDS loads, no registers and no ALU;
+//   2. each wavefront copies its tile's compressed block into LDS the same
+//      way, 16 bytes per lane, issued together with the table copy;
 //   3. each state reads its renormalisation words straight from the staged
 //      block at its own offset (a per-state LDS byte address that advances
 //      by 2 on each refill);
@@ -36,18 +37,9 @@ constexpr uint32_t kRansL = 1u << 16;
 constexpr int kMaxWaves = 8;
 constexpr int kMaxRB = 64;  // largest R*B compiled (16 * 4)
 
-// Table entry layout in LDS.  8 bytes (default): {freq | code<<24, bias},
-// one mad consumes both words and the code is the top byte.  4 bytes
-// (VRAMC_TABLE32=1): code | freq<<8 | bias<<20, one bit-field extract and
-// one shift more per symbol but half the LDS bank traffic of the lookup.
-#ifndef VRAMC_TABLE32
-#define VRAMC_TABLE32 0
-#endif
-#if VRAMC_TABLE32
-using TabEntry = uint32_t;
-#else
+// Table entry in LDS: {freq | code<<24, slot - cum}; one mad consumes both
+// words and the code is the sign-extended top byte.
 using TabEntry = uint2;
-#endif
 
 // LDS: the expanded table and the reduction scratch are static __shared__
 // arrays (their offsets are compile-time constants, so table addressing
@@ -55,10 +47,12 @@ using TabEntry = uint2;
 constexpr int kStaticLds =
     (int)sizeof(TabEntry) * (int)kProbM + 4 * kMaxWaves * kMaxRB + 4 * kMaxRB + 16;
 constexpr int kLdsMax = 160 * 1024;
+constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3 for gfx9 raw loads
 
 // 32-bit LDS addresses (address space 3), so a word read is one ds_read with
 // no base arithmetic.
 using lds_cu16 = const __attribute__((address_space(3))) uint16_t;
+using lds_void = __attribute__((address_space(3))) void;
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -78,7 +72,7 @@ struct GemvArgs {
     const uint32_t* tile_off;
     const uint16_t* soffs;
     const uint32_t* states;
-    const uint32_t* table;
+    const uint4* table_lds;  // 2048 x 16 B LDS image of the table
     const int32_t* esc_rowptr;
     const int32_t* esc_col;
     const int32_t* esc_val;
@@ -88,6 +82,7 @@ struct GemvArgs {
     float* partial;      // [ngroups][B][rows]
     uint32_t* counters;  // [rows/R]
     int rows, cols, C, ncb, ngroups;
+    int W;  // waves per workgroup (= blockDim.x / 64, as a kernel argument)
     WaveLayout L;
 };
 
@@ -96,110 +91,67 @@ struct DecodeArgs {
     const uint32_t* tile_off;
     const uint16_t* soffs;
     const uint32_t* states;
-    const uint32_t* table;
+    const uint4* table_lds;
     const float* step;
     void* out;
     int rows, cols, C, ncb, ntiles;
+    int W;  // waves per workgroup
     WaveLayout L;
 };
 
-// Reference-packed table entry (sym | freq<<8 | bias<<20) -> LDS entry;
-// the escape symbol (0) gets code 0 so it adds nothing in the GEMV and is
-// patched from the side table.
-__device__ __forceinline__ TabEntry expand_entry(uint32_t e) {
-    const uint32_t sym = e & 0xFFu;
-    const uint32_t code = sym == 0 ? 0u : (uint32_t)((int32_t)sym - 128);
-#if VRAMC_TABLE32
-    return (e & ~0xFFu) | (code & 0xFFu);
-#else
-    return make_uint2(((e >> 8) & 0xFFFu) | (code << 24), e >> 20);
-#endif
-}
-
 // freq*(st>>12) + bias (rans_gemv.cu:34): freq < 2^12 and st>>12 < 2^20
-// both fit the 24-bit multiplier.
+// both fit the 24-bit multiplier, whose operand ignores the code byte.
 __device__ __forceinline__ uint32_t entry_next_state(TabEntry e, uint32_t st) {
-#if VRAMC_TABLE32
-    return __umul24((e >> 8) & 0xFFFu, st >> 12) + (e >> 20);
-#else
     return __umul24(e.x, st >> 12) + e.y;
-#endif
 }
 
-__device__ __forceinline__ int32_t entry_code(TabEntry e) {
-#if VRAMC_TABLE32
-    return (int32_t)(int8_t)(e & 0xFFu);
-#else
-    return (int32_t)e.x >> 24;
-#endif
+__device__ __forceinline__ int32_t entry_code(TabEntry e) { return (int32_t)e.x >> 24; }
+
+// Direct global->LDS copy (global_load_lds_dwordx4): lane i's 16 bytes land
+// at the wave-uniform LDS address base + 16*i.  The copy is complete when
+// the wave's vector-memory counter has drained (wait_vm).
+__device__ __forceinline__ void copy16_to_lds(const uint4* src_lane, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(src_lane, (lds_void*)lds_wave_base, 16, 0, 0);
 }
 
-// Keeps the four registers of v live here: the loads that produce them
-// cannot be sunk below this point (next to the stores that use them).
-__device__ __forceinline__ void pin(const uint4& v) {
-    asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// The 32 KB table image: 32 chunks of 64 x 16 bytes, wave w of W copying
+// chunks w, w+W, ...  Issued after the tile block's copy: the table comes
+// from L2 (every workgroup reads it), the block from HBM, so the block's
+// copy is the one to start first.
+__device__ __forceinline__ void stage_table(TabEntry* tab, const uint4* __restrict__ img, int wave,
+                                            int W, int lane) {
+    for (int c = wave; c < 32; c += W)
+        copy16_to_lds(img + c * 64 + lane, reinterpret_cast<uint4*>(tab) + c * 64);
 }
 
-// Stages the expanded table (whole workgroup) and, for an active wave, its
-// tile block (a multiple of 8 words, at most raw_words) into LDS.  The
-// table loads and the first batch of tile loads are all issued before the
-// first LDS write, so the workgroup pays one memory latency.  Loads use
-// clamped indices (unconditional: a guarded load becomes a branch with its
-// own wait); stores are guarded, so no two lanes store to one address.
-__device__ __forceinline__ void stage_table_and_tile(TabEntry* tab, const uint32_t* __restrict__ table,
-                                                     uint16_t* raw,
-                                                     const uint16_t* __restrict__ words,
-                                                     const uint32_t* __restrict__ tile_off, int t,
-                                                     bool active, int lane, int raw_words) {
-    const uint4* tsrc = reinterpret_cast<const uint4*>(table);  // 1024 x 16 B
-    const int n = blockDim.x;                                    // 64 .. 512
-    const int tid = threadIdx.x;
-    uint4 tv[16];
-#pragma unroll
-    for (int j = 0; j < 16; j++) tv[j] = tsrc[min(tid + j * n, 1023)];
+// Extent of tile t's block: tile_off[t], tile_off[t+1] (loaded by every
+// lane; the wave-uniform values are taken by tile_extent, as late as
+// possible, so the loads issued in between are not waited for).
+struct TileOff {
+    uint32_t lo, hi;
+};
+__device__ __forceinline__ TileOff load_tile_off(const uint32_t* __restrict__ tile_off, int t) {
+    return {tile_off[t], tile_off[t + 1]};
+}
 
-    // tile extent, made explicitly wave-uniform (scalar loop control)
-    uint32_t o0 = 0, n16 = 0;
-    if (active) {
-        o0 = tile_off[t];
-        uint32_t nw = tile_off[t + 1] - o0;
-        if (nw > (uint32_t)raw_words) nw = (uint32_t)raw_words;
-        n16 = nw >> 3;
-    }
-    o0 = __builtin_amdgcn_readfirstlane(o0);
-    n16 = __builtin_amdgcn_readfirstlane(n16);
+// Start (in words) and length (in 16-byte units, at most the region) of the
+// block, as scalars; n16 is 0 for an inactive wave.
+__device__ __forceinline__ void tile_extent(TileOff to, bool active, int raw_words, uint32_t& o0,
+                                            uint32_t& n16) {
+    uint32_t nw = to.hi - to.lo;
+    if (nw > (uint32_t)raw_words) nw = (uint32_t)raw_words;
+    o0 = __builtin_amdgcn_readfirstlane(to.lo);
+    n16 = active ? __builtin_amdgcn_readfirstlane(nw >> 3) : 0u;
+}
+
+// The wave's tile block (n16 x 16 bytes at words + 8*o16) into its LDS region.
+__device__ __forceinline__ void stage_tile(uint16_t* raw, const uint16_t* __restrict__ words,
+                                           uint32_t o0, uint32_t n16, int lane) {
     const uint4* src = reinterpret_cast<const uint4*>(words + o0);
-    uint4* dst = reinterpret_cast<uint4*>(raw);
-    uint4 v[8];
-    if (n16) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = src[min((uint32_t)(lane + 64 * j), n16 - 1)];
-    }
-#pragma unroll
-    for (int j = 0; j < 16; j++) pin(tv[j]);
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-        const int i = tid + j * n;
-        if (i < 1024) {
-            tab[4 * i + 0] = expand_entry(tv[j].x);
-            tab[4 * i + 1] = expand_entry(tv[j].y);
-            tab[4 * i + 2] = expand_entry(tv[j].z);
-            tab[4 * i + 3] = expand_entry(tv[j].w);
-        }
-    }
-    for (uint32_t b = 0; b < n16; b += 512) {
-        if (b) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = src[min(b + lane + 64 * j, n16 - 1)];
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) pin(v[j]);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t i = b + lane + 64 * j;
-            if (i < n16) dst[i] = v[j];
-        }
-    }
+    for (uint32_t c = 0; c < n16; c += 64)
+        if (c + lane < n16) copy16_to_lds(src + c + lane, reinterpret_cast<uint4*>(raw) + c);
 }
 
 __device__ __forceinline__ uint32_t load_x_bits(const void* x, int64_t i, bool bf16) {
@@ -215,9 +167,21 @@ __device__ __forceinline__ float load_x(const void* x, int64_t i, bool bf16) {
     return bits_to_x(load_x_bits(x, i, bf16), bf16);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// v from lane (dpp CTRL) for the rows in ROWS; 0 in the other rows.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+
+// Sum over the 64 lanes with DPP moves (no LDS round trips); the total is
+// valid in lane 63.  Fixed order, so the result is deterministic.
+__device__ __forceinline__ float wave_sum63(float v) {
+    v += dpp<0xB1>(v);        // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);        // quad_perm [2,3,0,1]: quad sums
+    v += dpp<0x141>(v);       // row_half_mirror: sums of 8
+    v += dpp<0x140>(v);       // row_mirror: row (16-lane) sums
+    v += dpp<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+    v += dpp<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
     return v;
 }
 
@@ -272,52 +236,77 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     __shared__ int flag[4];
     extern __shared__ __align__(16) uint16_t dyn[];
     constexpr int nst = 64 * S;
-    const int W = blockDim.x >> 6;
+    const int W = a.W;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar tile math
     const int lane = threadIdx.x & 63;
     uint16_t* raw = dyn + (size_t)wave * a.L.wave_words;
 
     const int rb = blockIdx.x / a.ngroups;
     const int g = blockIdx.x - rb * a.ngroups;
-    const int cb = g * W + wave;
-    const bool active = cb < a.ncb;
+    const int cb = g * W + wave;  // W divides ncb: every wave has a tile
     const int t = rb * a.ncb + cb;
+    // Every kernel argument the prologue needs, fetched in one scalar batch
+    // (otherwise each is loaded, and waited for, at its first use).
+    asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.soffs), "s"(a.table_lds),
+                 "s"(a.words), "s"(a.x), "s"(a.step), "s"(a.esc_rowptr), "s"(a.C), "s"(a.cols),
+                 "s"(a.L.raw_words), "s"(a.W), "s"(a.ncb), "s"(a.ngroups));
 
     // Everything the wave needs from memory before decoding is requested in
     // one batch: initial states, stream offsets, the first block of x and
     // step, the table and the tile block.
     const int nk = a.C / nst;
     const int colbase = cb * a.C + lane;
+    // The tile extent is loaded first: the block copy waits for it, and
+    // loads complete in order, so nothing issued after it delays that copy.
+    const TileOff to = load_tile_off(a.tile_off, t);
     uint32_t st0[S], off0[S];
-    if (active) {
 #pragma unroll
-        for (int s = 0; s < S; s++) {
-            st0[s] = a.states[t * nst + 64 * s + lane];
-            off0[s] = a.soffs[t * nst + 64 * s + lane];
-        }
+    for (int s = 0; s < S; s++) {
+        st0[s] = a.states[t * nst + 64 * s + lane];
+        off0[s] = a.soffs[t * nst + 64 * s + lane];
     }
+    // Row pointers of this tile row's escapes (lanes 0..R), for the epilogue.
+    const int rp = a.esc_rowptr[rb * R + min(lane, R)];
     // x and step for KU column steps are loaded one block ahead of use, so
-    // their latency overlaps the decode of the current block.
+    // their latency overlaps the decode of the current block.  They are
+    // buffer loads ranged to one x row / the step vector: a block's columns
+    // are immediate offsets on one base register, and columns past the end
+    // of the matrix (the tail of the last block) read as 0.
     constexpr int KU = 4;
+    constexpr int XS = XBF16 ? 2 : 4;
+    __amdgpu_buffer_rsrc_t xrs[B];
+#pragma unroll
+    for (int b = 0; b < B; b++)
+        xrs[b] = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(static_cast<const uint8_t*>(a.x)) + (size_t)b * a.cols * XS, 0,
+            a.cols * XS, kBufWord3);
+    const __amdgpu_buffer_rsrc_t srs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.step), 0, a.cols * 4, kBufWord3);
     uint32_t xr[KU][S][B];  // raw bits: bf16 zero-extended, or f32
     float sr[KU][S];
     auto load_block = [&](int k0) {
+        const int c0 = colbase + 64 * S * k0;
 #pragma unroll
         for (int u = 0; u < KU; u++) {
-            const int k = k0 + u < nk ? k0 + u : nk - 1;
 #pragma unroll
             for (int s = 0; s < S; s++) {
-                const int col = colbase + 64 * (S * k + s);
-                sr[u][s] = a.step[col];
+                const int c = c0 + 64 * (S * u + s);
+                sr[u][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, c * 4, 0, 0));
 #pragma unroll
                 for (int b = 0; b < B; b++)
-                    xr[u][s][b] = load_x_bits(a.x, (int64_t)b * a.cols + col, XBF16);
+                    xr[u][s][b] =
+                        XBF16 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(xrs[b], c * 2, 0, 0)
+                              : __builtin_amdgcn_raw_buffer_load_b32(xrs[b], c * 4, 0, 0);
             }
         }
     };
-    if (active) load_block(0);
-    stage_table_and_tile(tab, a.table, raw, a.words, a.tile_off, t, active, lane, a.L.raw_words);
+    load_block(0);
+    uint32_t o0, n16;
+    tile_extent(to, true, a.L.raw_words, o0, n16);
+    stage_tile(raw, a.words, o0, n16, lane);
+    stage_table(tab, a.table_lds, wave, W, lane);
     if (threadIdx.x < R * B) esc_red[threadIdx.x] = 0.f;
+    wait_vm();
     __syncthreads();
 
     float acc[R][B];
@@ -326,7 +315,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
 #pragma unroll
         for (int b = 0; b < B; b++) acc[r][b] = 0.f;
 
-    if (active) {
+    {
         Lanes<S> L;
         init_lanes<S>(L, tab, raw, st0, off0);
         for (int k0 = 0; k0 < nk; k0 += KU) {
@@ -369,8 +358,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     // rows r = w, w+W, ..., its lanes stride over the row's side-table entries.
     if (g == 0) {
         for (int r = wave; r < R; r += W) {
-            const int row = rb * R + r;
-            const int e0 = a.esc_rowptr[row], e1 = a.esc_rowptr[row + 1];
+            const int e0 = __builtin_amdgcn_readlane(rp, r);
+            const int e1 = __builtin_amdgcn_readlane(rp, r + 1);
             if (e0 == e1) continue;
             float es[B];
 #pragma unroll
@@ -384,8 +373,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
             }
 #pragma unroll
             for (int b = 0; b < B; b++) {
-                const float v = wave_sum(es[b]);
-                if (lane == 0) esc_red[r * B + b] = v;
+                const float v = wave_sum63(es[b]);
+                if (lane == 63) esc_red[r * B + b] = v;
             }
         }
     }
@@ -394,8 +383,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     for (int r = 0; r < R; r++) {
 #pragma unroll
         for (int b = 0; b < B; b++) {
-            const float v = wave_sum(acc[r][b]);
-            if (lane == 0) red[wave * (R * B) + r * B + b] = v;
+            const float v = wave_sum63(acc[r][b]);
+            if (lane == 63) red[wave * (R * B) + r * B + b] = v;
         }
     }
     __syncthreads();
@@ -461,13 +450,14 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
     __shared__ __align__(16) TabEntry tab[kProbM];
     extern __shared__ __align__(16) uint16_t dyn[];
     constexpr int nst = 64 * S;
-    const int W = blockDim.x >> 6;
+    const int W = a.W;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar tile math
     const int lane = threadIdx.x & 63;
     uint16_t* raw = dyn + (size_t)wave * a.L.wave_words;
     const int t = blockIdx.x * W + wave;
     const bool active = t < a.ntiles;
 
+    const TileOff to = load_tile_off(a.tile_off, active ? t : a.ntiles - 1);
     uint32_t st0[S], off0[S];
     if (active) {
 #pragma unroll
@@ -476,7 +466,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
             off0[s] = a.soffs[t * nst + 64 * s + lane];
         }
     }
-    stage_table_and_tile(tab, a.table, raw, a.words, a.tile_off, t, active, lane, a.L.raw_words);
+    uint32_t o0, n16;
+    tile_extent(to, active, a.L.raw_words, o0, n16);
+    stage_tile(raw, a.words, o0, n16, lane);
+    stage_table(tab, a.table_lds, wave, W, lane);
+    wait_vm();
     __syncthreads();
     if (!active) return;
     Lanes<S> L;
@@ -547,8 +541,8 @@ __global__ void __launch_bounds__(256) int4_gemv_kernel(const uint32_t* __restri
                 acc = fmaf((float)((int)((qs[a] >> (4 * b)) & 15u) - 8), xs[b], acc);
         }
     }
-    acc = wave_sum(acc);
-    if (lane == 0) y[row] = acc;
+    acc = wave_sum63(acc);
+    if (lane == 63) y[row] = acc;
 }
 
 // ------------------------------------------------------------------ host
@@ -571,7 +565,7 @@ bool valid_geometry(const rans_w64_matrix* m) {
 }
 
 bool valid_pointers(const rans_w64_matrix* m) {
-    return m->words && m->tile_off && m->soffs && m->states && m->table && m->step &&
+    return m->words && m->tile_off && m->soffs && m->states && m->table_lds && m->step &&
            m->esc_rowptr && m->esc_col && m->esc_val;
 }
 
@@ -699,7 +693,7 @@ int launch_decode_common(const rans_w64_matrix* m, void* out, hipStream_t stream
     a.tile_off = m->tile_off;
     a.soffs = m->soffs;
     a.states = m->states;
-    a.table = m->table;
+    a.table_lds = reinterpret_cast<const uint4*>(m->table_lds);
     a.step = m->step;
     a.out = out;
     a.rows = m->rows;
@@ -707,6 +701,7 @@ int launch_decode_common(const rans_w64_matrix* m, void* out, hipStream_t stream
     a.C = m->C;
     a.ncb = m->cols / m->C;
     a.ntiles = (m->rows / m->R) * a.ncb;
+    a.W = waves;
     a.L = wave_layout(m);
     const int grid = (a.ntiles + waves - 1) / waves;
     int rc = dispatch_decode<MODE>(a, m->R, m->S, waves, lds_bytes(waves, a.L), grid, stream);
@@ -749,7 +744,7 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
     a.tile_off = m->tile_off;
     a.soffs = m->soffs;
     a.states = m->states;
-    a.table = m->table;
+    a.table_lds = reinterpret_cast<const uint4*>(m->table_lds);
     a.esc_rowptr = m->esc_rowptr;
     a.esc_col = m->esc_col;
     a.esc_val = m->esc_val;
@@ -759,6 +754,7 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
     a.C = m->C;
     a.ncb = ncb;
     a.ngroups = ngroups;
+    a.W = waves;
     a.L = wave_layout(m);
     a.counters = ngroups > 1 ? static_cast<uint32_t*>(m->workspace) : nullptr;
     a.partial = ngroups > 1

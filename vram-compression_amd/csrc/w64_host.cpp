@@ -92,6 +92,18 @@ extern "C" int rans_build_table(const uint8_t* sym, int64_t n, int64_t* freq, in
     return 0;
 }
 
+extern "C" int rans_table_lds(const uint32_t* table, uint32_t* out) {
+    if (!table || !out) return RANS_EARG;
+    for (uint32_t i = 0; i < kM; i++) {
+        const uint32_t e = table[i];
+        const uint32_t sym = e & 0xFFu;
+        const uint32_t code = sym == 0 ? 0u : (uint32_t)((int32_t)sym - 128);
+        out[2 * i] = ((e >> 8) & 0xFFFu) | (code << 24);
+        out[2 * i + 1] = e >> 20;
+    }
+    return 0;
+}
+
 extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols, int32_t R,
                                int32_t C, int32_t S, int32_t nthreads, void** handle,
                                int64_t* info) {

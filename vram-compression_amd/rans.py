@@ -49,14 +49,15 @@ class RansMatrixDesc(ctypes.Structure):
                 ("reserved", ctypes.c_int32),
                 ("words", ctypes.c_void_p), ("tile_off", ctypes.c_void_p),
                 ("soffs", ctypes.c_void_p), ("states", ctypes.c_void_p),
-                ("table", ctypes.c_void_p), ("esc_rowptr", ctypes.c_void_p),
+                ("table", ctypes.c_void_p), ("table_lds", ctypes.c_void_p),
+                ("esc_rowptr", ctypes.c_void_p),
                 ("esc_col", ctypes.c_void_p), ("esc_val", ctypes.c_void_p),
                 ("step", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
                 ("workspace_bytes", ctypes.c_int64)]
 
 
 EXPORTS = ("launch_rans_gemv", "rans_gemv_workspace_bytes", "launch_rans_decode",
-           "launch_rans_decode_codes", "launch_int4_gemv", "rans_build_table",
+           "launch_rans_decode_codes", "launch_int4_gemv", "rans_build_table", "rans_table_lds",
            "rans_w64_encode", "rans_w64_encode_fetch", "rans_w64_encode_free",
            "rans_w64_decode_host")
 
@@ -90,6 +91,7 @@ def load_lib(path=LIB):
         "launch_rans_decode_codes": ([D, P, P], ctypes.c_int),
         "launch_int4_gemv": ([P, P, P, ctypes.c_int, ctypes.c_int, P], ctypes.c_int),
         "rans_build_table": ([P, I64, P, P, P], ctypes.c_int),
+        "rans_table_lds": ([P, P], ctypes.c_int),
         "rans_w64_encode": ([P, I32, I32, I32, I32, I32, I32, ctypes.POINTER(P), P], ctypes.c_int),
         "rans_w64_encode_fetch": ([P] * 10, ctypes.c_int),
         "rans_w64_encode_free": ([P], None),
@@ -137,6 +139,17 @@ def build_table(sym):
     rc = _host_lib().rans_build_table(_p(s), s.size, _p(freq), _p(cum), _p(table))
     assert rc == 0, "degenerate distribution (single symbol)"
     return freq, cum, table
+
+
+def table_lds(table, lib=None):
+    """The 32 KB LDS image of a packed table (uint32[8192]): per slot
+    {freq | code<<24, slot - cum}, code 0 for the escape symbol."""
+    t = np.ascontiguousarray(np.asarray(table, np.uint32).ravel())
+    assert t.size == M, "table must have 4096 slots"
+    out = np.zeros(2 * M, np.uint32)
+    rc = (lib or _host_lib()).rans_table_lds(_p(t), _p(out))
+    assert rc == 0, f"rans_table_lds failed ({rc})"
+    return out
 
 
 # ------------------------------------------------------------------ encoding
@@ -256,7 +269,9 @@ class RansMatrix:
         self.tile_off = up(enc["tile_off"], np.int32)
         self.soffs = up(enc["soffs"], np.int16)
         self.states = up(enc["states"], np.int32)
-        self.table = up(enc["table"], np.int32)
+        # the kernels read the table's LDS image; the packed table is only
+        # for the host decoder and stays on the host
+        self.table_lds = up(table_lds(enc["table"], lib), np.int32)
         self.esc_rowptr = up(enc["esc_rowptr"], np.int32)
         # never hand a zero-length buffer's (possibly null) pointer to the ABI
         self.esc_col = up(enc["esc_col"] if len(enc["esc_col"]) else np.zeros(1, np.int32), np.int32)
@@ -271,13 +286,15 @@ class RansMatrix:
             max_tile_words=self.max_tile_words, max_state_words=self.max_state_words,
             words=self.words.data_ptr(), tile_off=self.tile_off.data_ptr(),
             soffs=self.soffs.data_ptr(), states=self.states.data_ptr(),
-            table=self.table.data_ptr(), esc_rowptr=self.esc_rowptr.data_ptr(),
+            table=None, table_lds=self.table_lds.data_ptr(),
+            esc_rowptr=self.esc_rowptr.data_ptr(),
             esc_col=self.esc_col.data_ptr(), esc_val=self.esc_val.data_ptr(),
             step=self.step.data_ptr(), workspace=None, workspace_bytes=0)
         self.workspace = None
         self._ensure_workspace(4)
+        # device bytes (the 32 KB table image in place of the 16 KB table)
         self.nbytes = sum(t.numel() * t.element_size() for t in
-                          (self.words, self.tile_off, self.soffs, self.states, self.table,
+                          (self.words, self.tile_off, self.soffs, self.states, self.table_lds,
                            self.esc_rowptr)) + 8 * int(len(enc["esc_col"]))
 
     def _ensure_workspace(self, batch):
