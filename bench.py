@@ -42,6 +42,14 @@ ROTATE_BYTES = 512 << 20
 # overhead.
 DEFAULT_TILING = (4, 2240, 1)
 
+# HBM traffic per launch of the headline kernel, from two rocprofv3 --pmc
+# passes (FETCH_SIZE, then WRITE_SIZE) over 50 rotated launches.  Each counter
+# is scaled by what it reads for an elementwise kernel that reads and writes
+# 256 MiB: reads x2.0, writes x1.0.  Commands and counts:
+# profiles/rans_w64_gemv_1536x8960_3.25b.md.  Keyed by (R, C, S, word fetch).
+PMC_TRAFFIC_KIB = {(4, 2240, 1, "always"): (3432.2, 12.0)}
+PMC_FETCH_FACTOR, PMC_WRITE_FACTOR = 2.0, 1.0
+
 
 def algorithmic_bytes(enc, rows, cols, batch=1):
     """Bytes one GEMV must move: the whole compressed matrix as the device
@@ -123,6 +131,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--tiling", type=str, default=None, help="R,C,S")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--word-fetch", choices=("tune", "always", "refill"), default="tune",
+                    help="GEMV word-fetch policy; 'tune' times both on the matrix")
     ap.add_argument("--no-rocblas", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="print a tiling sweep to stderr")
     ap.add_argument("--profile", action="store_true",
@@ -145,17 +155,25 @@ def main():
     step_t = torch.from_numpy(step)
     print(f"workload ready: entropy {B.entropy_fast(codes):.4f} bits", file=sys.stderr, flush=True)
 
+    def pick_fetch(m):
+        if args.word_fetch == "tune":
+            return m.tune()
+        return rans.F_WORDS_ALWAYS if args.word_fetch == "always" else rans.F_WORDS_REFILL
+
     def measure(R, C, S, steps):
         enc = rans.encode(codes, R, C, S)
         comp, alg = algorithmic_bytes(enc, ROWS, COLS)
         ncopy = max(2, -(-ROTATE_BYTES // comp))
-        ms = [rans.RansMatrix(enc, step_t, lib) for _ in range(ncopy)]
+        m0 = rans.RansMatrix(enc, step_t, lib)
+        flags = pick_fetch(m0)
+        ms = [m0] + [rans.RansMatrix(enc, step_t, lib, flags=flags) for _ in range(ncopy - 1)]
         y = torch.empty(ROWS, device="cuda")
         fns = [lambda m=m: m.gemv(xb, y) for m in ms]
         t_rot = graph_time_us(fns, steps, args.warmup)
         t_hot = graph_time_us(fns[:1], steps, args.warmup)
-        del ms
+        del ms, m0
         torch.cuda.empty_cache()
+        measure.flags = flags
         return enc, comp, alg, ncopy, t_rot, t_hot
 
     if args.profile:
@@ -163,7 +181,9 @@ def main():
         enc = rans.encode(codes, R, C, S)
         comp, alg = algorithmic_bytes(enc, ROWS, COLS)
         ncopy = max(2, -(-ROTATE_BYTES // comp))
-        ms = [rans.RansMatrix(enc, step_t, lib) for _ in range(ncopy)]
+        m0 = rans.RansMatrix(enc, step_t, lib)
+        flags = pick_fetch(m0)
+        ms = [m0] + [rans.RansMatrix(enc, step_t, lib, flags=flags) for _ in range(ncopy - 1)]
         y = torch.empty(ROWS, device="cuda")
         for i in range(args.warmup + args.steps):
             ms[i % ncopy].gemv(xb, y)
@@ -174,7 +194,8 @@ def main():
         torch.cuda.synchronize()
         torch.neg(src, out=dst)
         torch.cuda.synchronize()
-        print(json.dumps({"profile": True, "R": R, "C": C, "S": S, "launches": args.warmup + args.steps,
+        print(json.dumps({"profile": True, "R": R, "C": C, "S": S, "flags": flags,
+                          "launches": args.warmup + args.steps,
                           "copies": ncopy, "algorithmic_bytes_per_launch": alg,
                           "compressed_bytes": comp, "calibration_copy_bytes": 256 << 20}), flush=True)
         return
@@ -234,6 +255,10 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline(codes, step, torch.from_numpy(x).bfloat16().float().numpy())
 
     achieved = alg / (t_rot * 1e-6) / 1e9
+    fetch_name = {rans.F_WORDS_ALWAYS: "always", rans.F_WORDS_REFILL: "refill"}.get(measure.flags)
+    pmc = PMC_TRAFFIC_KIB.get((R, C, S, fetch_name))
+    traffic = None if pmc is None else \
+        int((pmc[0] * PMC_FETCH_FACTOR + pmc[1] * PMC_WRITE_FACTOR) * 1024)
     out = {
         "metric": METRIC,
         "value": ROWS * COLS * 2 / t_rot / 1e3,
@@ -252,6 +277,7 @@ def main():
                    "rows": ROWS, "cols": COLS, "batch": 1, "R": R, "C": C, "S": S,
                    "states": int(len(enc["states"])), "bits_total": bits_total,
                    "bits_payload": enc["bits_payload"], "rotating_copies": ncopy,
+                   "word_fetch": {1: "always", 2: "refill"}.get(measure.flags, "default"),
                    "parallelism": "single GPU"},
         "us_per_gemv": t_rot,
         "hot_us_per_gemv": t_hot,
@@ -259,7 +285,10 @@ def main():
         "compressed_GBps": comp / t_rot / 1e3,
         "rocblas_bf16": rocblas,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "traffic_source": None if traffic is None else
+                     "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, scaled x2.0 / x1.0 "
+                     "(profiles/rans_w64_gemv_1536x8960_3.25b.md)",
                      "kernel": "rans_w64_gemv_kernel", "bytes_per_launch": alg},
         "cpu_baseline": cpu,
     }

@@ -62,13 +62,20 @@ extern "C" {
 #define RANS_ECODES (-5)       /* encoder: degenerate or empty symbol distribution */
 #define RANS_ETILE (-6)        /* encoder: a tile block exceeds 65535 words */
 
+/* rans_w64_matrix.flags: how the GEMV fetches renormalisation words.  The
+ * decoded values are identical; only speed differs.  0 = library default
+ * (REFILL for R >= 8, ALWAYS otherwise). */
+#define RANS_F_WORDS_ALWAYS 1 /* every lane re-reads its next word each step */
+#define RANS_F_WORDS_REFILL 2 /* only lanes that consumed their word fetch the next */
+#define RANS_F_WORDS_MASK 3
+
 typedef struct rans_w64_matrix {
     int32_t rows, cols;       /* out_features, in_features */
     int32_t R, C, S;          /* tile rows, tile columns, states per lane */
     int32_t max_tile_words;   /* largest tile block, in 16-bit words */
     int32_t max_state_words;  /* longest state stream (to the next state's start, the
                                  last state of a tile to the end of its padded block) */
-    int32_t reserved;         /* keeps the pointers 8-byte aligned; set to 0 */
+    int32_t flags;            /* RANS_F_* launch options, 0 for the defaults */
     const uint16_t* words;    /* [tile_off[ntiles]] */
     const uint32_t* tile_off; /* [ntiles+1], in words, multiples of 8 */
     const uint16_t* soffs;    /* [ntiles*64*S] */

@@ -59,6 +59,10 @@ def test_argument_validation_without_gpu(rans, lib):
     assert lib.rans_gemv_workspace_bytes(ctypes.byref(one), 1) == 0
     huge = _desc(rans, mtw=70000)
     assert lib.rans_gemv_workspace_bytes(ctypes.byref(huge), 1) == -2
+    for flags in (3, 4, -1):  # both word-fetch bits, or an unknown bit
+        bad_flags = _desc(rans, cols=2048)
+        bad_flags.flags = flags
+        assert lib.launch_rans_gemv(ctypes.byref(bad_flags), x, 0, 1, y, None) == -2
     no_img = _desc(rans)
     no_img.table_lds = None  # the kernels need the table's LDS image
     assert lib.launch_rans_gemv(ctypes.byref(no_img), x, 0, 1, y, None) == -4

@@ -209,3 +209,29 @@ def test_int4_baseline(rans, lib, dev):
     y_ref = torch.from_numpy(codes).double().cuda() @ (x.double() * step.double().cuda())
     y = m4.gemv(x)
     assert torch.allclose(y.double(), y_ref, rtol=1e-4, atol=1e-3)
+
+
+@pytest.mark.parametrize("R,C,S", [(4, 256, 1), (8, 512, 2), (16, 128, 1), (2, 256, 4)])
+def test_word_fetch_policies_agree(rans, oracle, lib, dev, R, C, S):
+    """Both word-fetch policies of the GEMV (every lane re-reads each step,
+    or only lanes that consumed their word) decode the same symbols in the
+    same order: outputs are bitwise equal, and match the oracle."""
+    rows, cols = 256, 1024
+    print(f"case word fetch R={R} C={C} S={S}", flush=True)
+    codes = oracle.synth_codes(rows, cols, 3.25, seed=R * 100 + S)
+    codes[5, 7] = 300  # one escape
+    rng = np.random.default_rng(R)
+    step = (rng.random(cols) + 0.5).astype(np.float32)
+    enc = rans.encode(codes, R, C, S)
+    x = torch.from_numpy(rng.standard_normal((4, cols)).astype(np.float32)).cuda().bfloat16()
+    ys = []
+    for flags in (rans.F_WORDS_ALWAYS, rans.F_WORDS_REFILL, 0):
+        m = rans.RansMatrix(enc, torch.from_numpy(step), lib, flags=flags)
+        ys.append(m.gemv(x).cpu())
+    assert torch.equal(ys[0], ys[1]) and torch.equal(ys[0], ys[2])
+    m = rans.RansMatrix(enc, torch.from_numpy(step), lib)
+    assert m.tune(batch=4) in (rans.F_WORDS_ALWAYS, rans.F_WORDS_REFILL)
+    assert torch.equal(m.gemv(x).cpu(), ys[0])
+    ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64),
+                          step.astype(np.float64))
+    assert _rel_l2(ys[0].numpy(), ref) <= REL_L2

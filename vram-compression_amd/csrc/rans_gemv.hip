@@ -216,6 +216,13 @@ __device__ __forceinline__ void init_lanes(Lanes<S>& L, const TabEntry* tab, con
 // entry for the following symbol is read as soon as the new state exists,
 // before the code conversion and the word-pointer update, so those overlap
 // the LDS latency instead of sitting on the state's dependency chain.
+//
+// The next word w is always read ahead.  REFILL=false: every lane re-reads
+// it each step (no divergence, the cheapest step when LDS is not the
+// bottleneck).  REFILL=true: only the lanes that just consumed their word
+// fetch the next one (an EXEC-masked read, about 1 lane in 5 at 3 bits per
+// symbol), which cuts LDS bank traffic where many waves share the CU.
+template <bool REFILL>
 __device__ __forceinline__ int32_t rans_step(uint32_t& st, uint32_t& a, uint32_t& w, TabEntry& e,
                                              const TabEntry* tab) {
     const TabEntry cur = e;
@@ -223,12 +230,19 @@ __device__ __forceinline__ int32_t rans_step(uint32_t& st, uint32_t& a, uint32_t
     const bool need = ns < kRansL;
     st = need ? ((ns << 16) | w) : ns;
     e = tab[st & (kProbM - 1)];
-    a += need ? 2u : 0u;
-    w = lds_read_u16(a);
+    if (REFILL) {
+        if (need) {
+            a += 2u;
+            w = lds_read_u16(a);
+        }
+    } else {
+        a += need ? 2u : 0u;
+        w = lds_read_u16(a);
+    }
     return entry_code(cur);
 }
 
-template <int R, int S, int B, bool XBF16>
+template <int R, int S, int B, bool XBF16, bool REFILL>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs a) {
     __shared__ __align__(16) TabEntry tab[kProbM];
     __shared__ float red[kMaxWaves * kMaxRB];
@@ -344,7 +358,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
                 for (int r = 0; r < R; r++) {
 #pragma unroll
                     for (int s = 0; s < S; s++) {
-                        const float code = (float)rans_step(L.st[s], L.a[s], L.w[s], L.e[s], tab);
+                        const float code =
+                        (float)rans_step<REFILL>(L.st[s], L.a[s], L.w[s], L.e[s], tab);
 #pragma unroll
                         for (int b = 0; b < B; b++)
                             acc[r][b] = fmaf(code, xv[u][s][b], acc[r][b]);
@@ -487,7 +502,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
 #pragma unroll
             for (int s = 0; s < S; s++) {
                 const int col = colbase + 64 * (S * k + s);
-                const int32_t code = rans_step(L.st[s], L.a[s], L.w[s], L.e[s], tab);
+                const int32_t code = rans_step<(R >= 8)>(L.st[s], L.a[s], L.w[s], L.e[s], tab);
                 const int64_t o = ((int64_t)rb * R + r) * a.cols + col;
                 if (MODE == 0)
                     reinterpret_cast<int32_t*>(a.out)[o] = code;
@@ -557,7 +572,9 @@ WaveLayout wave_layout(const rans_w64_matrix* m) {
 size_t lds_bytes(int waves, const WaveLayout& L) { return (size_t)waves * L.wave_words * 2; }
 
 bool valid_geometry(const rans_w64_matrix* m) {
-    if (!m || m->rows <= 0 || m->cols <= 0 || m->R <= 0 || m->C <= 0 || m->S <= 0) return false;
+    if (!m || (m->flags & ~RANS_F_WORDS_MASK) || (m->flags & RANS_F_WORDS_MASK) == RANS_F_WORDS_MASK)
+        return false;
+    if (m->rows <= 0 || m->cols <= 0 || m->R <= 0 || m->C <= 0 || m->S <= 0) return false;
     if (m->rows % m->R || m->cols % m->C || m->C % (64 * m->S)) return false;
     if (m->max_tile_words <= 0 || m->max_tile_words > 65536) return false;
     if (m->max_state_words <= 0 || m->max_state_words > m->max_tile_words) return false;
@@ -606,51 +623,55 @@ hipError_t ensure_lds(const void* fn, size_t bytes) {
     return e;
 }
 
-template <int R, int S, int B, bool XBF16>
+template <int R, int S, int B, bool XBF16, bool REFILL>
 int launch_gemv_t(const GemvArgs& a, int waves, size_t lds, int grid, hipStream_t stream) {
-    const void* fn = reinterpret_cast<const void*>(&rans_w64_gemv_kernel<R, S, B, XBF16>);
+    const void* fn = reinterpret_cast<const void*>(&rans_w64_gemv_kernel<R, S, B, XBF16, REFILL>);
     hipError_t e = ensure_lds(fn, lds);
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((rans_w64_gemv_kernel<R, S, B, XBF16>), dim3(grid), dim3(64 * waves), lds,
-                       stream, a);
+    hipLaunchKernelGGL((rans_w64_gemv_kernel<R, S, B, XBF16, REFILL>), dim3(grid), dim3(64 * waves),
+                       lds, stream, a);
     return (int)hipGetLastError();
 }
 
+// var: bit 0 = bf16 x, bit 1 = refill-only word fetch.
 template <int R, int S, int B>
-int dispatch_x(const GemvArgs& a, bool xbf16, int waves, size_t lds, int grid, hipStream_t st) {
-    return xbf16 ? launch_gemv_t<R, S, B, true>(a, waves, lds, grid, st)
-                 : launch_gemv_t<R, S, B, false>(a, waves, lds, grid, st);
+int dispatch_v(const GemvArgs& a, int var, int waves, size_t lds, int grid, hipStream_t st) {
+    switch (var) {
+        case 0: return launch_gemv_t<R, S, B, false, false>(a, waves, lds, grid, st);
+        case 1: return launch_gemv_t<R, S, B, true, false>(a, waves, lds, grid, st);
+        case 2: return launch_gemv_t<R, S, B, false, true>(a, waves, lds, grid, st);
+        default: return launch_gemv_t<R, S, B, true, true>(a, waves, lds, grid, st);
+    }
 }
 
 template <int R, int S>
-int dispatch_b(const GemvArgs& a, int B, bool xbf16, int waves, size_t lds, int grid,
-               hipStream_t st) {
+int dispatch_b(const GemvArgs& a, int B, int var, int waves, size_t lds, int grid, hipStream_t st) {
     switch (B) {
-        case 1: return dispatch_x<R, S, 1>(a, xbf16, waves, lds, grid, st);
-        case 4: return dispatch_x<R, S, 4>(a, xbf16, waves, lds, grid, st);
+        case 1: return dispatch_v<R, S, 1>(a, var, waves, lds, grid, st);
+        case 4: return dispatch_v<R, S, 4>(a, var, waves, lds, grid, st);
         default: return RANS_EUNSUPPORTED;
     }
 }
 
 template <int R>
-int dispatch_s(const GemvArgs& a, int S, int B, bool xbf16, int waves, size_t lds, int grid,
+int dispatch_s(const GemvArgs& a, int S, int B, int var, int waves, size_t lds, int grid,
                hipStream_t st) {
     switch (S) {
-        case 1: return dispatch_b<R, 1>(a, B, xbf16, waves, lds, grid, st);
-        case 2: return dispatch_b<R, 2>(a, B, xbf16, waves, lds, grid, st);
-        case 4: return dispatch_b<R, 4>(a, B, xbf16, waves, lds, grid, st);
+        case 1: return dispatch_b<R, 1>(a, B, var, waves, lds, grid, st);
+        case 2: return dispatch_b<R, 2>(a, B, var, waves, lds, grid, st);
+        case 4: return dispatch_b<R, 4>(a, B, var, waves, lds, grid, st);
         default: return RANS_EUNSUPPORTED;
     }
 }
 
-int dispatch_gemv(const GemvArgs& a, int R, int S, int B, bool xbf16, int waves, size_t lds,
-                  int grid, hipStream_t st) {
+int dispatch_gemv(const GemvArgs& a, int R, int S, int B, int var, int waves, size_t lds, int grid,
+                  hipStream_t st) {
     switch (R) {
-        case 1: return dispatch_s<1>(a, S, B, xbf16, waves, lds, grid, st);
-        case 2: return dispatch_s<2>(a, S, B, xbf16, waves, lds, grid, st);
-        case 4: return dispatch_s<4>(a, S, B, xbf16, waves, lds, grid, st);
-        case 8: return dispatch_s<8>(a, S, B, xbf16, waves, lds, grid, st);
-        case 16: return dispatch_s<16>(a, S, B, xbf16, waves, lds, grid, st);
+        case 1: return dispatch_s<1>(a, S, B, var, waves, lds, grid, st);
+        case 2: return dispatch_s<2>(a, S, B, var, waves, lds, grid, st);
+        case 4: return dispatch_s<4>(a, S, B, var, waves, lds, grid, st);
+        case 8: return dispatch_s<8>(a, S, B, var, waves, lds, grid, st);
+        case 16: return dispatch_s<16>(a, S, B, var, waves, lds, grid, st);
         default: return RANS_EUNSUPPORTED;
     }
 }
@@ -738,6 +759,9 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
         return RANS_EWORKSPACE;
     const bool xbf16 = x_dtype == RANS_X_BF16;
     const size_t xsz = xbf16 ? 2 : 4;
+    const int fetch = m->flags & RANS_F_WORDS_MASK;
+    const bool refill = fetch == RANS_F_WORDS_REFILL || (fetch == 0 && m->R >= 8);
+    const int var = (xbf16 ? 1 : 0) | (refill ? 2 : 0);
 
     GemvArgs a;
     a.words = m->words;
@@ -769,7 +793,7 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
         const int B = batch - done >= 4 ? 4 : 1;
         a.x = static_cast<const uint8_t*>(x) + (size_t)done * m->cols * xsz;
         a.y = static_cast<float*>(y) + (size_t)done * m->rows;
-        const int rc = dispatch_gemv(a, m->R, m->S, B, xbf16, waves, lds, grid, stream);
+        const int rc = dispatch_gemv(a, m->R, m->S, B, var, waves, lds, grid, stream);
         if (rc != 0) return rc;
         done += B;
     }

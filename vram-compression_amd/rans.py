@@ -35,6 +35,8 @@ ESC = 0  # escape symbol: codes outside [-127, 127]
 LANES = 64
 
 X_F32, X_BF16 = 0, 1
+# rans_w64_matrix.flags: word fetch of the GEMV (0 = library default)
+F_WORDS_ALWAYS, F_WORDS_REFILL = 1, 2
 
 HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared",
                # packed fp32 VALU ops stay disabled on this platform
@@ -46,7 +48,7 @@ class RansMatrixDesc(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_int32), ("cols", ctypes.c_int32),
                 ("R", ctypes.c_int32), ("C", ctypes.c_int32), ("S", ctypes.c_int32),
                 ("max_tile_words", ctypes.c_int32), ("max_state_words", ctypes.c_int32),
-                ("reserved", ctypes.c_int32),
+                ("flags", ctypes.c_int32),
                 ("words", ctypes.c_void_p), ("tile_off", ctypes.c_void_p),
                 ("soffs", ctypes.c_void_p), ("states", ctypes.c_void_p),
                 ("table", ctypes.c_void_p), ("table_lds", ctypes.c_void_p),
@@ -253,7 +255,9 @@ def _require_gpu():
 class RansMatrix:
     """Entropy-coded matrix resident on the GPU (rans.py:127-162)."""
 
-    def __init__(self, enc, step, lib):
+    def __init__(self, enc, step, lib, flags=0):
+        """flags: F_WORDS_ALWAYS / F_WORDS_REFILL picks the GEMV's word
+        fetch (same results, different speed); 0 lets the library choose."""
         _require_gpu()
         if lib is None:
             raise RuntimeError("librans_hip.so not loaded")
@@ -284,7 +288,7 @@ class RansMatrix:
         self._desc = RansMatrixDesc(
             rows=self.rows, cols=self.cols, R=self.R, C=self.C, S=self.S,
             max_tile_words=self.max_tile_words, max_state_words=self.max_state_words,
-            words=self.words.data_ptr(), tile_off=self.tile_off.data_ptr(),
+            flags=int(flags), words=self.words.data_ptr(), tile_off=self.tile_off.data_ptr(),
             soffs=self.soffs.data_ptr(), states=self.states.data_ptr(),
             table=None, table_lds=self.table_lds.data_ptr(),
             esc_rowptr=self.esc_rowptr.data_ptr(),
@@ -296,6 +300,47 @@ class RansMatrix:
         self.nbytes = sum(t.numel() * t.element_size() for t in
                           (self.words, self.tile_off, self.soffs, self.states, self.table_lds,
                            self.esc_rowptr)) + 8 * int(len(enc["esc_col"]))
+
+    def tune(self, batch=1, x_dtype=torch.bfloat16, iters=20):
+        """Time the two word-fetch policies of the GEMV on this matrix and
+        keep the faster one.  Both give bitwise identical results; which is
+        faster depends on the tile geometry and the matrix size.  Each
+        policy's launches are captured in a HIP graph and replayed, so the
+        events time back-to-back kernels rather than host launch overhead.
+        Returns the chosen flag."""
+        x = torch.randn(batch, self.cols, device="cuda").to(x_dtype)
+        y = torch.empty(batch, self.rows, device="cuda")
+        best = None
+        for f in (F_WORDS_ALWAYS, F_WORDS_REFILL):
+            self._desc.flags = f
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                self.gemv(x, y)  # first launch of this kernel outside the capture
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(iters):
+                    self.gemv(x, y)
+            g.replay()
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record()
+            g.replay()
+            g.replay()
+            t1.record()
+            t1.synchronize()
+            t = t0.elapsed_time(t1)
+            del g
+            if best is None or t < best[0]:
+                best = (t, f)
+        self._desc.flags = best[1]
+        return best[1]
+
+    @property
+    def flags(self):
+        return int(self._desc.flags)
 
     def _ensure_workspace(self, batch):
         need = int(self.lib.rans_gemv_workspace_bytes(ctypes.byref(self._desc), batch))

@@ -162,26 +162,41 @@ def timeit_graph(fns, iters=200, warmup=10):
 # ---------------------------------------------------------------- harness
 def pick_tiling(rows, cols, R=None, S=1, target_states=None):
     """A legal (R, C) for the w64 format: C a multiple of 64*S dividing cols,
-    R in {1, 2, 4, 8, 16}, chosen so about `target_states` states cover the
-    matrix (fewer states mean less per-state overhead, more mean more
-    parallelism).  Tilings whose 4..8 column tiles fill one workgroup are
-    preferred: fewer waves per workgroup repeat the table staging more often,
-    more column tiles than 8 need the split-K reduction."""
+    R in {1, 2, 4, 8, 16}.  Chosen by measurement on MI355X:
+
+    - states: about 140 symbols per state for mid-size matrices (~98K
+      states); small ones get more states, down to 64 symbols each, so the
+      chip has about one wavefront per SIMD; matrices above 32M weights use
+      about 160 symbols per state.  Fewer states cost less per-state
+      overhead (48 bits each), more states give more parallelism.
+    - column tiles per tile row (ncb): 8 is best (8 waves of a workgroup
+      share one LDS table, so more waves fit per CU), then 4-7 and 16 (the
+      latter needs the split-K reduction); fewer than 4 repeat the table
+      staging more often per tile."""
     nst = 64 * S
     cands = [c for c in range(nst, cols + 1, nst) if cols % c == 0]
     assert cands, f"cols={cols} has no divisor that is a multiple of {nst}"
     Rs = [R] if R else [r for r in (16, 8, 4, 2, 1) if rows % r == 0]
-    # about 140 symbols per state; small matrices get more states (down to
-    # 64 symbols each) so the chip has about one wavefront per SIMD, large
-    # ones stop at what saturates it (about 3 per SIMD)
     n = rows * cols
-    target = target_states or int(min(max(n // 140, min(98304, n // 64)), 262144))
+    if target_states:
+        target = target_states
+    elif n >= (32 << 20):
+        target = n // 160
+    else:
+        target = int(min(max(n // 140, min(98304, n // 64)), 262144))
     best = None
     for r in Rs:
         for c in cands:
             states = (rows // r) * (cols // c) * nst
             ncb = cols // c
-            penalty = 0.0 if 4 <= ncb <= 8 else (0.35 if ncb < 4 else 0.5)
+            if ncb == 8:
+                penalty = 0.0
+            elif 4 <= ncb <= 7:
+                penalty = 0.3 if n >= (32 << 20) else 0.0
+            elif ncb == 16:
+                penalty = 0.2
+            else:
+                penalty = 0.35 if ncb < 4 else 0.5
             key = (abs(np.log(states / target)) + penalty, -c)
             if best is None or key < best[0]:
                 best = (key, r, c)
@@ -300,8 +315,9 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
         R, C = pick_tiling(rows, cols, S=S)
     enc = encode(codes, R, C, S)
     m = rans.RansMatrix(enc, step, lib)
+    flags = m.tune(batch=batch)
     ncopy = max(2, -(-rotate_bytes // m.nbytes))
-    ms = [m] + [rans.RansMatrix(enc, step, lib) for _ in range(ncopy - 1)]
+    ms = [m] + [rans.RansMatrix(enc, step, lib, flags=flags) for _ in range(ncopy - 1)]
     x = torch.randn(batch, cols, device="cuda").bfloat16()
     y = torch.empty(batch, rows, device="cuda")
     t_rans = timeit_graph([lambda mm=mm: mm.gemv(x, y) for mm in ms], iters)
@@ -313,7 +329,8 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
     got = ms[0].gemv(x)
     err = float((got - ref).norm() / ref.norm())
     out = dict(rows=rows, cols=cols, bits_target=bits, dist=dist, escape_frac=escape_frac,
-               batch=batch, R=R, C=C, S=S, entropy=entropy_fast(codes),
+               batch=batch, R=R, C=C, S=S, word_fetch={1: "always", 2: "refill"}[flags],
+               entropy=entropy_fast(codes),
                bits_total=8 * m.nbytes / codes.size, n_escapes=int(len(enc["esc_col"])),
                t_rans_us=t_rans, t_bf16_us=t_bf16,
                effective_GBps=rows * cols * 2 / t_rans / 1e3,
@@ -336,6 +353,7 @@ def chain(bits=3.25, layers=28, seed=0, iters=3):
     nweights = 0
     # one step per shape, chosen on a sample, so every layer has ~`bits` bits
     deltas = {}
+    fetch = {}
     for name, rows, cols in qwen15b_layer_shapes():
         sample = rng.laplace(size=1 << 20)
         lo, hi = -12.0, 6.0
@@ -350,7 +368,10 @@ def chain(bits=3.25, layers=28, seed=0, iters=3):
             step = torch.from_numpy(lognormal_steps(cols, seed=seed + layer))
             R, C = chain_tiling(rows, cols)
             enc = encode(codes, R, C, 1)
-            m = rans.RansMatrix(enc, step, lib)
+            # word-fetch policy tuned once per shape, on the first layer
+            m = rans.RansMatrix(enc, step, lib, flags=fetch.get(name, 0))
+            if name not in fetch:
+                fetch[name] = m.tune()
             mats.append(m)
             nbytes += m.nbytes
             nweights += codes.size
