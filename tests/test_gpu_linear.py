@@ -1,0 +1,77 @@
+"""RansLinear on the GPU: the nn.Linear drop-in against a dense fp32
+reference, and a tiny random-init Qwen2 model with every projection
+replaced (fp32 model: attention stays out of bf16 batched products)."""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return float((a - b).norm() / b.norm())
+
+
+def test_ranslinear_matches_dense(rans, lib):
+    import rans_linear as L
+    print("case RansLinear 512x1536", flush=True)
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(512, 1536, generator=g) * 0.02
+    b = torch.randn(512, generator=g)
+    codes, step = L.quantize_uniform(w, 4.0)
+    codes[7, 9] = 400  # an escape
+    lin = L.RansLinear.from_codes(codes, step, b, lib)
+    wd = torch.from_numpy(codes).double() * torch.from_numpy(step).double()
+    tol = {torch.float32: 1e-3, torch.bfloat16: 8e-3, torch.float16: 2e-3}
+    for shape in [(1536,), (3, 1536), (2, 5, 1536)]:
+        for dt in (torch.float32, torch.bfloat16, torch.float16):
+            x = torch.randn(shape, generator=g).to(dt)
+            y = lin(x.cuda())
+            ref = torch.nn.functional.linear(x.double(), wd) + b.double()
+            assert y.dtype == dt and tuple(y.shape) == tuple(ref.shape)
+            assert _rel(y, ref) <= tol[dt], (shape, dt, _rel(y, ref))
+    # prefill-sized batch: bf16 decode + dense GEMM
+    x = torch.randn(32, 1536, generator=g)
+    y = lin(x.cuda())
+    ref = torch.nn.functional.linear(x.double(), wd) + b.double()
+    assert _rel(y, ref) <= 1e-2
+
+
+def test_tiny_qwen2_with_rans_linears(rans, lib):
+    import rans_linear as L
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    print("case tiny Qwen2, all projections rANS-coded", flush=True)
+    cfg = Qwen2Config(vocab_size=512, hidden_size=256, intermediate_size=512,
+                      num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                      max_position_embeddings=128)
+    torch.manual_seed(0)
+    dense = Qwen2ForCausalLM(cfg).eval()
+    coded = copy.deepcopy(dense)
+    names = L.replace_linears(coded, bits=6.0, lib=lib, tune=False)
+    assert len(names) == 2 * 7  # q, k, v, o, gate, up, down per layer; lm_head stays dense
+    # the dense twin gets exactly the dequantised weights code*step (fp32)
+    for n in names:
+        m = coded.get_submodule(n).matrix
+        wq = m.decode_codes().float() * m.step.reshape(1, -1)
+        dense.get_submodule(n).weight.data.copy_(wq.cpu())
+    dense, coded = dense.cuda(), coded.cuda()
+    ids = torch.randint(0, 512, (1, 12), generator=torch.Generator().manual_seed(1)).cuda()
+    with torch.no_grad():
+        a = dense(ids).logits
+        b = coded(ids).logits
+        assert _rel(b, a) <= 1e-3
+        # greedy token loop with the KV cache: same tokens from both models
+        out_d, out_c = dense(ids, use_cache=True), coded(ids, use_cache=True)
+        pd, pc = out_d.past_key_values, out_c.past_key_values
+        td = tc = ids[:, -1:]
+        for _ in range(6):
+            td = out_d.logits[:, -1:].argmax(-1)
+            tc = out_c.logits[:, -1:].argmax(-1)
+            assert torch.equal(td, tc)
+            out_d = dense(td, past_key_values=pd, use_cache=True)
+            out_c = coded(tc, past_key_values=pc, use_cache=True)
+            pd, pc = out_d.past_key_values, out_c.past_key_values
+            assert _rel(out_c.logits, out_d.logits) <= 1e-3

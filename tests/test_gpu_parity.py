@@ -235,3 +235,23 @@ def test_word_fetch_policies_agree(rans, oracle, lib, dev, R, C, S):
     ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64),
                           step.astype(np.float64))
     assert _rel_l2(ys[0].numpy(), ref) <= REL_L2
+
+
+def test_matrix_from_container_file(rans, oracle, lib, dev, tmp_path):
+    """A matrix saved with rans_io and memory-mapped back gives the same
+    GEMV, bit for bit, as the in-memory encoding, with the stored flags."""
+    import rans_io
+    print("case container round trip 512x2048", flush=True)
+    codes = oracle.synth_codes(512, 2048, 3.25, seed=11)
+    codes[1, 2] = -500
+    step = (np.random.default_rng(5).random(2048) + 0.5).astype(np.float32)
+    enc = rans.encode(codes, 8, 512, 1)
+    path = str(tmp_path / "m.w64")
+    rans_io.save(path, [dict(name="m", enc=enc, step=step, flags=rans.F_WORDS_REFILL)])
+    (e,) = rans_io.load(path)
+    a = rans.RansMatrix(enc, torch.from_numpy(step), lib)
+    b = rans.RansMatrix(e["enc"], torch.from_numpy(np.array(e["step"])), lib, flags=e["flags"])
+    assert b.flags == rans.F_WORDS_REFILL
+    x = torch.randn(2048, device="cuda").bfloat16()
+    assert torch.equal(a.gemv(x), b.gemv(x))
+    np.testing.assert_array_equal(b.decode_codes().cpu().numpy(), codes)

@@ -21,7 +21,7 @@ import torch
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 import rans  # noqa: E402
-from rans import encode  # noqa: E402
+from rans import encode, pick_tiling  # noqa: E402,F401
 
 RES = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "results")
 
@@ -160,49 +160,6 @@ def timeit_graph(fns, iters=200, warmup=10):
 
 
 # ---------------------------------------------------------------- harness
-def pick_tiling(rows, cols, R=None, S=1, target_states=None):
-    """A legal (R, C) for the w64 format: C a multiple of 64*S dividing cols,
-    R in {1, 2, 4, 8, 16}.  Chosen by measurement on MI355X:
-
-    - states: about 140 symbols per state for mid-size matrices (~98K
-      states); small ones get more states, down to 64 symbols each, so the
-      chip has about one wavefront per SIMD; matrices above 32M weights use
-      about 160 symbols per state.  Fewer states cost less per-state
-      overhead (48 bits each), more states give more parallelism.
-    - column tiles per tile row (ncb): 8 is best (8 waves of a workgroup
-      share one LDS table, so more waves fit per CU), then 4-7 and 16 (the
-      latter needs the split-K reduction); fewer than 4 repeat the table
-      staging more often per tile."""
-    nst = 64 * S
-    cands = [c for c in range(nst, cols + 1, nst) if cols % c == 0]
-    assert cands, f"cols={cols} has no divisor that is a multiple of {nst}"
-    Rs = [R] if R else [r for r in (16, 8, 4, 2, 1) if rows % r == 0]
-    n = rows * cols
-    if target_states:
-        target = target_states
-    elif n >= (32 << 20):
-        target = n // 160
-    else:
-        target = int(min(max(n // 140, min(98304, n // 64)), 262144))
-    best = None
-    for r in Rs:
-        for c in cands:
-            states = (rows // r) * (cols // c) * nst
-            ncb = cols // c
-            if ncb == 8:
-                penalty = 0.0
-            elif 4 <= ncb <= 7:
-                penalty = 0.3 if n >= (32 << 20) else 0.0
-            elif ncb == 16:
-                penalty = 0.2
-            else:
-                penalty = 0.35 if ncb < 4 else 0.5
-            key = (abs(np.log(states / target)) + penalty, -c)
-            if best is None or key < best[0]:
-                best = (key, r, c)
-    return best[1], best[2]
-
-
 def test():
     """The reference's test (bench.py:38-66) on the w64 layout."""
     lib = rans.build()

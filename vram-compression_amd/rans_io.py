@@ -1,0 +1,175 @@
+"""On-disk container for w64-encoded matrices (one or many per file).
+
+The reference keeps encoded matrices only in memory (kernel/rans.py:62-98
+returns a dict, kernel/bench.py re-encodes on every run).  A 1.31 G-weight
+set takes minutes to encode, so it is stored once and memory-mapped on load:
+every array is a zero-copy view of the file, ready to upload.
+
+Layout (all integers little endian, every section 64-byte aligned):
+
+    header, 64 bytes
+        magic      8 bytes  b"VRAMCW64"
+        version    u32      1
+        nmat       u32      number of matrices
+        index_off  u64      byte offset of the index
+        file_bytes u64      total file size (truncation check)
+        reserved   32 bytes zero
+    index, nmat records of 256 bytes
+        name       64 bytes UTF-8, NUL padded
+        rows, cols, R, C, S, max_tile_words, max_state_words, flags   i32 x 8
+        nwords, ntiles, nstates, nesc, payload_words                  u64 x 5
+        entropy_model                                                 f64
+        offsets of words, tile_off, soffs, states, table, esc_rowptr,
+                   esc_col, esc_val, step                             u64 x 9
+        crc32 of the nine sections, in that order                     u32
+        zero padding to 256 bytes
+    sections
+        words u16[nwords], tile_off u32[ntiles+1], soffs u16[nstates],
+        states u32[nstates], table u32[4096] (reference packing),
+        esc_rowptr i32[rows+1], esc_col i32[nesc], esc_val i32[nesc],
+        step f32[cols]
+
+`flags` is the GEMV word-fetch policy chosen for the matrix (0 = library
+default), so a tuned set reloads with its tuning.
+"""
+import os
+import struct
+import zlib
+
+import numpy as np
+
+import rans
+
+MAGIC = b"VRAMCW64"
+VERSION = 1
+_HEADER = struct.Struct("<8sIIQQ32x")
+_RECORD = struct.Struct("<64s8i5Qd9QI")
+RECORD_BYTES = 256
+ALIGN = 64
+_SECTIONS = (("words", np.uint16), ("tile_off", np.uint32), ("soffs", np.uint16),
+             ("states", np.uint32), ("table", np.uint32), ("esc_rowptr", np.int32),
+             ("esc_col", np.int32), ("esc_val", np.int32), ("step", np.float32))
+assert _HEADER.size == 64 and _RECORD.size <= RECORD_BYTES
+
+
+def _align(n):
+    return (n + ALIGN - 1) // ALIGN * ALIGN
+
+
+def _section_lengths(rows, cols, nwords, ntiles, nstates, nesc):
+    return dict(words=nwords, tile_off=ntiles + 1, soffs=nstates, states=nstates,
+                table=rans.M, esc_rowptr=rows + 1, esc_col=nesc, esc_val=nesc, step=cols)
+
+
+def save(path, entries):
+    """Write `entries` (a list of dicts with keys name, enc, step and
+    optionally flags) to `path`.  enc is the dict rans.encode returns; step
+    is the per-column f32 step vector.  Writes to a temporary name and
+    renames, so a reader never sees a partial file."""
+    recs, blobs = [], []
+    pos = _align(_HEADER.size + RECORD_BYTES * len(entries))
+    for e in entries:
+        enc = e["enc"]
+        rows, cols = (int(v) for v in enc["shape"])
+        arrays = {}
+        for key, dt in _SECTIONS:
+            a = e["step"] if key == "step" else enc[key]
+            arrays[key] = np.ascontiguousarray(np.asarray(a).reshape(-1), dtype=dt)
+        n = _section_lengths(rows, cols, arrays["words"].size, arrays["tile_off"].size - 1,
+                             arrays["states"].size, arrays["esc_col"].size)
+        for key, _ in _SECTIONS:
+            assert arrays[key].size == n[key], f"{e['name']}: {key} has {arrays[key].size} " \
+                                               f"entries, expected {n[key]}"
+        payload_words = int(round(enc["bits_payload"] * rows * cols / 16))
+        offs, crc = [], 0
+        for key, _ in _SECTIONS:
+            offs.append(pos)
+            b = arrays[key].tobytes()
+            crc = zlib.crc32(b, crc)
+            blobs.append((pos, b))
+            pos = _align(pos + len(b))
+        name = e["name"].encode("utf-8")
+        assert len(name) <= 64, "matrix names are at most 64 bytes of UTF-8"
+        recs.append(_RECORD.pack(name, rows, cols, enc["R"], enc["C"], enc["S"],
+                                 enc["max_tile_words"], enc["max_state_words"],
+                                 int(e.get("flags", 0)), arrays["words"].size,
+                                 arrays["tile_off"].size - 1, arrays["states"].size,
+                                 arrays["esc_col"].size, payload_words,
+                                 float(enc.get("entropy_model", 0.0)), *offs, crc))
+    total = pos
+    tmp = f"{path}.tmp{os.getpid()}"
+    with open(tmp, "wb") as f:
+        f.write(_HEADER.pack(MAGIC, VERSION, len(entries), _HEADER.size, total))
+        for r in recs:
+            f.write(r.ljust(RECORD_BYTES, b"\0"))
+        for off, b in blobs:
+            f.seek(off)
+            f.write(b)
+        f.truncate(total)
+    os.replace(tmp, path)
+    return total
+
+
+def load(path, verify=True, mmap=True):
+    """Read a container written by `save`.  Returns a list of dicts with
+    keys name, enc (the dict rans.encode returns, arrays as read-only views
+    of the file when mmap), step and flags.  Raises ValueError on a wrong
+    magic or version, a truncated file, a section outside the file, or (with
+    verify) a CRC mismatch."""
+    size = os.path.getsize(path)
+    with open(path, "rb") as f:
+        head = f.read(_HEADER.size)
+        if len(head) < _HEADER.size:
+            raise ValueError("not a w64 container: file shorter than its header")
+        magic, version, nmat, index_off, file_bytes = _HEADER.unpack(head)
+        if magic != MAGIC:
+            raise ValueError("not a w64 container: bad magic")
+        if version != VERSION:
+            raise ValueError(f"unsupported w64 container version {version}")
+        if file_bytes != size:
+            raise ValueError(f"truncated or padded file: header says {file_bytes} bytes, "
+                             f"file has {size}")
+        if index_off + RECORD_BYTES * nmat > size:
+            raise ValueError("index runs past the end of the file")
+        f.seek(index_off)
+        raw = f.read(RECORD_BYTES * nmat)
+    buf = np.memmap(path, dtype=np.uint8, mode="r") if mmap else np.fromfile(path, np.uint8)
+    out = []
+    for i in range(nmat):
+        v = _RECORD.unpack(raw[i * RECORD_BYTES:i * RECORD_BYTES + _RECORD.size])
+        name = v[0].rstrip(b"\0").decode("utf-8")
+        rows, cols, R, C, S, mtw, msw, flags = v[1:9]
+        nwords, ntiles, nstates, nesc, payload_words = v[9:14]
+        entropy_model = v[14]
+        offs = v[15:24]
+        crc_want = v[24]
+        if rows <= 0 or cols <= 0 or R <= 0 or C <= 0 or S <= 0 or rows % R or cols % C \
+                or C % (64 * S) or ntiles != (rows // R) * (cols // C) \
+                or nstates != ntiles * 64 * S:
+            raise ValueError(f"{name}: inconsistent geometry in the index")
+        n = _section_lengths(rows, cols, nwords, ntiles, nstates, nesc)
+        arrays, crc = {}, 0
+        for (key, dt), off in zip(_SECTIONS, offs):
+            nbytes = n[key] * np.dtype(dt).itemsize
+            if off % ALIGN or off + nbytes > size:
+                raise ValueError(f"{name}: section {key} lies outside the file")
+            a = buf[off:off + nbytes]
+            if verify:
+                crc = zlib.crc32(a, crc)
+            arrays[key] = a.view(dt)
+        if verify and crc != crc_want:
+            raise ValueError(f"{name}: CRC mismatch (file corrupted)")
+        N = rows * cols
+        pad = nwords - payload_words
+        enc = dict(words=arrays["words"], tile_off=arrays["tile_off"], soffs=arrays["soffs"],
+                   states=arrays["states"], table=arrays["table"],
+                   esc_rowptr=arrays["esc_rowptr"], esc_col=arrays["esc_col"],
+                   esc_val=arrays["esc_val"], R=R, C=C, S=S, shape=(rows, cols),
+                   max_tile_words=mtw, max_state_words=msw,
+                   bits_payload=16 * payload_words / N,
+                   bits_state_offs=(48 * nstates + 32 * (ntiles + 1) + 16 * pad) / N,
+                   bits_table=32 * rans.M / N,
+                   bits_escape=32 * (rows + 1 + 2 * nesc) / N,
+                   entropy_model=entropy_model)
+        out.append(dict(name=name, enc=enc, step=arrays["step"], flags=flags))
+    return out

@@ -1,0 +1,127 @@
+"""torch.nn.Linear drop-in whose weight stays rANS-coded in HBM.
+
+The reference names model integration as its next step (README.md:39) and
+stops at the kernel.  RansLinear is that step: forward(x) runs the fused
+decode+GEMV kernel for decode-sized batches and, for large batches
+(prefill), decodes the weight to bf16 once and calls the dense GEMM, which
+is then the faster path.  Inference only: the weight is not a parameter.
+
+quantize_uniform is a plain uniform quantiser (one step per tensor, chosen
+for a target code entropy) so that ordinary nn.Linear layers can be
+converted in tests and demos; the reference's ECSQ-GPTQ quantiser
+(exp/quant.py) is outside this repository.
+"""
+import numpy as np
+import torch
+
+import rans
+
+PREFILL_ROWS = 16  # batches above this decode the weight and use the dense GEMM
+
+
+def _entropy(codes):
+    _, counts = np.unique(codes, return_counts=True)
+    p = counts / counts.sum()
+    return float(-(p * np.log2(p)).sum())
+
+
+def quantize_uniform(weight, bits, iters=40, sample=1 << 22, seed=0):
+    """codes = round(W / delta) with one delta per tensor, bisected on a
+    sample of W (all of it when small) so that the codes' empirical entropy
+    is `bits`.  Returns (int32 codes, f32 step vector of one value per
+    input column)."""
+    w = torch.as_tensor(weight).detach().float().cpu().numpy()
+    flat = w.ravel()
+    if flat.size > sample:
+        flat = np.random.default_rng(seed).choice(flat, sample, replace=False)
+    scale = float(np.abs(flat).max()) or 1.0
+    lo, hi = np.log(scale) - 20.0, np.log(scale) + 1.0
+    for _ in range(iters):
+        mid = (lo + hi) / 2
+        h = _entropy(np.round(flat / np.exp(mid)).astype(np.int64))
+        lo, hi = (mid, hi) if h > bits else (lo, mid)
+    delta = float(np.exp((lo + hi) / 2))
+    codes = np.round(w / delta).astype(np.int32)
+    return codes, np.full(w.shape[1], delta, np.float32)
+
+
+class RansLinear(torch.nn.Module):
+    """y = x @ W^T + b with W = code * step held as a rans.RansMatrix."""
+
+    def __init__(self, matrix, bias=None):
+        super().__init__()
+        self.matrix = matrix
+        self.in_features = matrix.cols
+        self.out_features = matrix.rows
+        if bias is not None:
+            b = torch.as_tensor(bias).detach().float().reshape(self.out_features)
+            self.register_buffer("bias", b.to("cuda"))
+        else:
+            self.bias = None
+
+    @classmethod
+    def from_codes(cls, codes, step, bias=None, lib=None, tiling=None, tune=True):
+        """codes (out x in ints), step (in,) f32.  tiling: (R, C, S) or None
+        for rans.pick_tiling; tune: pick the word-fetch policy by timing."""
+        codes = np.ascontiguousarray(codes, dtype=np.int32)
+        rows, cols = codes.shape
+        if tiling is None:
+            R, C = rans.pick_tiling(rows, cols)
+            S = 1
+        else:
+            R, C, S = tiling
+        lib = lib or rans.build()
+        m = rans.RansMatrix(rans.encode(codes, R, C, S), torch.as_tensor(step), lib)
+        if tune:
+            m.tune()
+        return cls(m, bias)
+
+    @classmethod
+    def from_linear(cls, linear, bits=3.25, lib=None, tiling=None, tune=True):
+        """Quantise an nn.Linear with quantize_uniform and encode it."""
+        codes, step = quantize_uniform(linear.weight, bits)
+        bias = None if linear.bias is None else linear.bias.detach()
+        return cls.from_codes(codes, step, bias, lib, tiling, tune)
+
+    def forward(self, x):
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"expected last dim {self.in_features}, got {x.shape[-1]}")
+        lead = x.shape[:-1]
+        xd = x.reshape(-1, self.in_features)
+        if xd.dtype not in (torch.bfloat16, torch.float32):
+            xd = xd.float()
+        if xd.shape[0] > PREFILL_ROWS:
+            w = self.matrix.decode()  # bf16 code*step, then the dense GEMM
+            y = torch.nn.functional.linear(xd.to(torch.bfloat16), w).float()
+        else:
+            y = self.matrix.gemv(xd.contiguous())
+        if self.bias is not None:
+            y = y + self.bias
+        out_dtype = x.dtype if x.dtype in (torch.bfloat16, torch.float16, torch.float32) \
+            else torch.float32
+        return y.to(out_dtype).reshape(*lead, self.out_features)
+
+    def extra_repr(self):
+        m = self.matrix
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}, tiles={m.R}x{m.C}x{m.S}, "
+                f"bits_per_weight={8 * m.nbytes / (m.rows * m.cols):.3f}")
+
+
+def replace_linears(module, bits=3.25, lib=None, skip=("lm_head",), tune=True):
+    """Swap every nn.Linear of `module` (except names containing an entry of
+    `skip`) for a RansLinear quantised at `bits`.  Returns the names swapped.
+    Layers whose in_features is not a multiple of 64 (the w64 tile width)
+    are left dense."""
+    lib = lib or rans.build()
+    done = []
+    for name, child in list(module.named_modules()):
+        for cname, sub in list(child.named_children()):
+            full = f"{name}.{cname}" if name else cname
+            if not isinstance(sub, torch.nn.Linear) or any(s in full for s in skip):
+                continue
+            if sub.in_features % 64:
+                continue
+            setattr(child, cname, RansLinear.from_linear(sub, bits, lib, tune=tune))
+            done.append(full)
+    return done
