@@ -121,7 +121,65 @@ def cpu_baseline(codes, step, x, budget_s=12.0):
                        f"{codes.size} symbols = {t_decode_full:.1f} s, plus numpy dense GEMV "
                        f"{t_gemv * 1e3:.1f} ms on {blas} BLAS threads"),
             "us_per_gemv": t * 1e6, "host_cpus": len(os.sched_getaffinity(0)),
-            "numpy": np.__version__}
+            "numpy": np.__version__,
+            "per_config": cpu_per_config(oracle, per_sym, t_gemv / codes.size)}
+
+
+def _gemv_seconds(rows, cols, reps=3):
+    W = np.ones((rows, cols), np.float32)
+    xs = np.ones(cols, np.float32)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        W @ xs
+    return (time.perf_counter() - t0) / reps
+
+
+def cpu_per_config(oracle, metric_ns_per_symbol, metric_gemv_s_per_weight, budget_s=2.0):
+    """The same CPU path on the other workloads: configurations 1-3 timed
+    on a bounded sample of lanes of their reference 32-lane encoding (one
+    tile row; codes outside [-128, 127] clipped to the reference alphabet)
+    plus the full numpy GEMV; configurations 4-5 extrapolated from measured
+    per-symbol and per-weight rates, and labelled so."""
+    out = []
+
+    def timed(name, codes, R, C, rows, cols):
+        enc = oracle.encode_ref(np.clip(codes, -128, 127), R, C)
+        n = (C // 32) * R
+        t0 = time.perf_counter()
+        oracle.decode_ref_py(enc, max_lanes=2)
+        per_lane = (time.perf_counter() - t0) / 2
+        lanes = int(max(2, min(len(enc["offs"]), budget_s / max(per_lane, 1e-9))))
+        t0 = time.perf_counter()
+        oracle.decode_ref_py(enc, max_lanes=lanes)
+        per_sym = (time.perf_counter() - t0) / (lanes * n)
+        t_gemv = _gemv_seconds(rows, cols)
+        t = per_sym * rows * cols + t_gemv
+        out.append({"config": name, "kind": "measured sample", "us_per_gemv": t * 1e6,
+                    "ns_per_symbol": per_sym * 1e9,
+                    "sample": f"{lanes * n} symbols of R={R} C={C} lanes, full numpy GEMV"})
+        return per_sym
+
+    c1 = B.synth_codes_full(512, 256, 3.25, seed=512 + 256)
+    timed("1: 512x256 Laplace 3.25 b (reference CPU test path, R=512 C=256, 32 lanes)",
+          c1, 512, 256, 512, 256)
+    c2 = B.synth_codes_full(1536, 1536, 4.25, dist="gauss", seed=3072)
+    timed("2: q_proj 1536x1536 N(0,1) 4.25 b", c2[:8], 8, 1536, 1536, 1536)
+    c3 = B.synth_codes_full(8960, 1536, 2.25, seed=8960 + 1536, escape_frac=0.001)
+    r3 = timed("3: gate/up 8960x1536 Laplace 2.25 b", c3[:8], 8, 1536, 8960, 1536)
+    c3d = B.synth_codes_full(1536, 8960, 2.25, seed=8960 + 1536 + 1, escape_frac=0.001)
+    timed("3: down 1536x8960 Laplace 2.25 b", c3d[:8], 8, 8960, 1536, 8960)
+    n4 = 28 * (2 * 1536 * 1536 + 2 * 256 * 1536 + 3 * 8960 * 1536)
+    out.append({"config": "4: 196-GEMV Qwen2.5-1.5B-shaped chain, 3.25 b",
+                "kind": "extrapolated", "us_per_gemv": None,
+                "us_per_chain": n4 * (metric_ns_per_symbol * 1e-9 + metric_gemv_s_per_weight) * 1e6,
+                "sample": f"{n4} symbols at the metric shape's measured rate"})
+    for shape in ((25600, 5120), (5120, 25600)):
+        n5 = shape[0] * shape[1]
+        out.append({"config": f"5: {shape[0]}x{shape[1]} Student-t 2.25 b, B=1",
+                    "kind": "extrapolated",
+                    "us_per_gemv": n5 * (r3 + metric_gemv_s_per_weight) * 1e6,
+                    "sample": f"{n5} symbols at configuration 3's measured rate"})
+    return out
 
 
 def main():

@@ -214,8 +214,10 @@ def decode_ref_py(enc, max_lanes=None):
     rows, cols = enc["shape"]
     R, C = enc["R"], enc["C"]
     tab = enc["table"].astype(np.int64).tolist()
-    w = enc["words"].astype(np.int64).tolist()
     lanes = len(enc["offs"]) if max_lanes is None else min(max_lanes, len(enc["offs"]))
+    # lanes' streams are consecutive: a sample converts only the words it reads
+    end = len(enc["words"]) if lanes == len(enc["offs"]) else int(enc["offs"][lanes])
+    w = enc["words"][:end].astype(np.int64).tolist()
     n = (C // 32) * R
     S = np.zeros((lanes, n), np.int64)
     for li in range(lanes):

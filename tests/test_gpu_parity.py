@@ -255,3 +255,41 @@ def test_matrix_from_container_file(rans, oracle, lib, dev, tmp_path):
     x = torch.randn(2048, device="cuda").bfloat16()
     assert torch.equal(a.gemv(x), b.gemv(x))
     np.testing.assert_array_equal(b.decode_codes().cpu().numpy(), codes)
+
+
+def _heavy_tail_codes(rows, cols, seed):
+    """Student-t(3) codes at about 3 bits with 1% escapes (|code| in
+    [128, 600)), generated fast enough for 131M weights."""
+    rng = np.random.default_rng(seed)
+    pool = np.rint(rng.standard_t(3, size=1 << 22) * 1.4).astype(np.int32)
+    codes = pool[rng.integers(0, pool.size, size=rows * cols)]
+    esc = rng.random(rows * cols) < 0.01
+    k = int(esc.sum())
+    codes[esc] = rng.integers(128, 600, size=k) * np.where(rng.random(k) < 0.5, -1, 1)
+    return codes.reshape(rows, cols)
+
+
+@pytest.mark.parametrize("rows,cols", [(25600, 5120), (5120, 25600)])
+def test_full_size_27b_shapes(rans, oracle, lib, dev, rows, cols):
+    """The 27B-class shapes at full size (131M weights, ~1.3M escapes):
+    every code bit-exact, GEMV at batch 1 and 4 against the float64 oracle,
+    both word-fetch policies bitwise equal."""
+    print(f"case full size {rows}x{cols}", flush=True)
+    codes = _heavy_tail_codes(rows, cols, seed=rows)
+    R, C = rans.pick_tiling(rows, cols)
+    enc = rans.encode(codes, R, C, 1)
+    step = np.exp(0.5 * np.random.default_rng(cols).standard_normal(cols)).astype(np.float32)
+    m = rans.RansMatrix(enc, torch.from_numpy(step), lib)
+    got = m.decode_codes().cpu().numpy()
+    assert np.array_equal(got, codes)
+    del got
+    x = torch.randn(4, cols, device="cuda").bfloat16()
+    ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64),
+                          step.astype(np.float64))
+    m._desc.flags = rans.F_WORDS_ALWAYS
+    y4 = m.gemv(x).cpu()
+    y1 = m.gemv(x[0]).cpu()
+    m._desc.flags = rans.F_WORDS_REFILL
+    assert torch.equal(m.gemv(x).cpu(), y4)
+    assert _rel_l2(y4.numpy(), ref) <= REL_L2
+    assert _rel_l2(y1.numpy(), ref[0]) <= REL_L2
