@@ -134,7 +134,7 @@ def _gemv_seconds(rows, cols, reps=3):
     return (time.perf_counter() - t0) / reps
 
 
-def cpu_per_config(oracle, metric_ns_per_symbol, metric_gemv_s_per_weight, budget_s=2.0):
+def cpu_per_config(oracle, metric_s_per_symbol, metric_gemv_s_per_weight, budget_s=2.0):
     """The same CPU path on the other workloads: configurations 1-3 timed
     on a bounded sample of lanes of their reference 32-lane encoding (one
     tile row; codes outside [-128, 127] clipped to the reference alphabet)
@@ -171,7 +171,7 @@ def cpu_per_config(oracle, metric_ns_per_symbol, metric_gemv_s_per_weight, budge
     n4 = 28 * (2 * 1536 * 1536 + 2 * 256 * 1536 + 3 * 8960 * 1536)
     out.append({"config": "4: 196-GEMV Qwen2.5-1.5B-shaped chain, 3.25 b",
                 "kind": "extrapolated", "us_per_gemv": None,
-                "us_per_chain": n4 * (metric_ns_per_symbol * 1e-9 + metric_gemv_s_per_weight) * 1e6,
+                "us_per_chain": n4 * (metric_s_per_symbol + metric_gemv_s_per_weight) * 1e6,
                 "sample": f"{n4} symbols at the metric shape's measured rate"})
     for shape in ((25600, 5120), (5120, 25600)):
         n5 = shape[0] * shape[1]
