@@ -44,8 +44,7 @@ using TabEntry = uint2;
 // LDS: the expanded table and the reduction scratch are static __shared__
 // arrays (their offsets are compile-time constants, so table addressing
 // needs no base add); the per-wave regions are dynamic.
-constexpr int kStaticLds =
-    (int)sizeof(TabEntry) * (int)kProbM + 4 * kMaxWaves * kMaxRB + 4 * kMaxRB + 16;
+constexpr int kStaticLds = (int)sizeof(TabEntry) * (int)kProbM + 4 * kMaxWaves * kMaxRB + 16;
 constexpr int kLdsMax = 160 * 1024;
 constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3 for gfx9 raw loads
 
@@ -114,7 +113,9 @@ __device__ __forceinline__ void copy16_to_lds(const uint4* src_lane, void* lds_w
     __builtin_amdgcn_global_load_lds(src_lane, (lds_void*)lds_wave_base, 16, 0, 0);
 }
 
-__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima), as a builtin
+// so the compiler's own wait tracking knows every vector load is complete.
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // The 32 KB table image: 32 chunks of 64 x 16 bytes, wave w of W copying
 // chunks w, w+W, ...  Issued after the tile block's copy: the table comes
@@ -242,11 +243,24 @@ __device__ __forceinline__ int32_t rans_step(uint32_t& st, uint32_t& a, uint32_t
     return entry_code(cur);
 }
 
+// Adds escape entry e (of this tile row's CSR range, rp holding the row
+// pointers of rows rb*R .. rb*R+R in lanes 0..R) to the lane's accumulator
+// of its row; v[b] is value*step*x[b] (0 for a lane without an entry).
+template <int R, int B>
+__device__ __forceinline__ void add_escape(float (&acc)[R][B], int rp, int e, const float (&v)[B]) {
+    int re = 0;
+#pragma unroll
+    for (int r = 1; r < R; r++) re += e >= __builtin_amdgcn_readlane(rp, r) ? 1 : 0;
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < B; b++) acc[r][b] += re == r ? v[b] : 0.f;
+}
+
 template <int R, int S, int B, bool XBF16, bool REFILL>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs a) {
     __shared__ __align__(16) TabEntry tab[kProbM];
     __shared__ float red[kMaxWaves * kMaxRB];
-    __shared__ float esc_red[kMaxRB];
     __shared__ int flag[4];
     extern __shared__ __align__(16) uint16_t dyn[];
     constexpr int nst = 64 * S;
@@ -262,7 +276,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     // Every kernel argument the prologue needs, fetched in one scalar batch
     // (otherwise each is loaded, and waited for, at its first use).
     asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.soffs), "s"(a.table_lds),
-                 "s"(a.words), "s"(a.x), "s"(a.step), "s"(a.esc_rowptr), "s"(a.C), "s"(a.cols),
+                 "s"(a.words), "s"(a.x), "s"(a.step), "s"(a.esc_rowptr), "s"(a.esc_col),
+                 "s"(a.esc_val), "s"(a.C), "s"(a.cols),
                  "s"(a.L.raw_words), "s"(a.W), "s"(a.ncb), "s"(a.ngroups));
 
     // Everything the wave needs from memory before decoding is requested in
@@ -273,20 +288,21 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     // The tile extent is loaded first: the block copy waits for it, and
     // loads complete in order, so nothing issued after it delays that copy.
     const TileOff to = load_tile_off(a.tile_off, t);
+    // Row pointers of this tile row's escapes (lanes 0..R), also needed early.
+    const int rp = a.esc_rowptr[rb * R + min(lane, R)];
+    asm volatile("" ::: "memory");  // keep these two loads first
     uint32_t st0[S], off0[S];
 #pragma unroll
     for (int s = 0; s < S; s++) {
         st0[s] = a.states[t * nst + 64 * s + lane];
         off0[s] = a.soffs[t * nst + 64 * s + lane];
     }
-    // Row pointers of this tile row's escapes (lanes 0..R), for the epilogue.
-    const int rp = a.esc_rowptr[rb * R + min(lane, R)];
     // x and step for KU column steps are loaded one block ahead of use, so
     // their latency overlaps the decode of the current block.  They are
     // buffer loads ranged to one x row / the step vector: a block's columns
     // are immediate offsets on one base register, and columns past the end
     // of the matrix (the tail of the last block) read as 0.
-    constexpr int KU = 4;
+    constexpr int KU = S >= 4 ? 2 : 4;  // 8 (column, state) groups in flight at S=2 and S=4
     constexpr int XS = XBF16 ? 2 : 4;
     __amdgpu_buffer_rsrc_t xrs[B];
 #pragma unroll
@@ -317,37 +333,78 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     load_block(0);
     uint32_t o0, n16;
     tile_extent(to, true, a.L.raw_words, o0, n16);
+    // Escapes of this tile row are added by column group 0, in chunks of 64
+    // side-table entries: chunk k goes to wave k mod W.  The row pointers
+    // are read here, before the copies, while the wait for them is exact;
+    // the wave's first chunk is requested behind the copies (so waiting for
+    // it costs nothing more), and its x and step gathers go out before the
+    // decode loop, their values kept raw until after the loop, so that
+    // latency overlaps the decode.
+    const int e_lo = g == 0 ? __builtin_amdgcn_readlane(rp, 0) : 0;
+    const int e_hi = g == 0 ? __builtin_amdgcn_readlane(rp, R) : 0;
+    asm volatile("" ::"s"(e_lo), "s"(e_hi));
     stage_tile(raw, a.words, o0, n16, lane);
     stage_table(tab, a.table_lds, wave, W, lane);
-    if (threadIdx.x < R * B) esc_red[threadIdx.x] = 0.f;
+    constexpr int P = 2;  // chunks per wave prefetched: up to 64*P*W escapes per tile row
+    int ecol[P], eval[P];
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        ecol[p] = eval[p] = 0;
+        if (e_lo + 64 * (wave + p * W) < e_hi) {  // wave-uniform
+            const int ec = min(e_lo + 64 * (wave + p * W) + lane, e_hi - 1);
+            ecol[p] = a.esc_col[ec];
+            eval[p] = a.esc_val[ec];
+        }
+    }
     wait_vm();
     __syncthreads();
-
     float acc[R][B];
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int b = 0; b < B; b++) acc[r][b] = 0.f;
 
+    // x*step of the current block, converted at the top of each iteration.
+    float xv[KU][S][B];
+    auto convert = [&]() {
+#pragma unroll
+        for (int u = 0; u < KU; u++)
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                // pin the prefetched registers here so the multiply is not
+                // hoisted next to their loads
+                asm volatile("" : "+v"(sr[u][s]));
+#pragma unroll
+                for (int b = 0; b < B; b++) {
+                    asm volatile("" : "+v"(xr[u][s][b]));
+                    xv[u][s][b] = bits_to_x(xr[u][s][b], XBF16) * sr[u][s];
+                }
+            }
+    };
+    // Escape gathers: issued in the first iteration behind the prefetch of
+    // the second block, so the first wait that can drain them comes a block
+    // of decode later.  Unconditional (column 0 for a wave without a chunk):
+    // no branch, so no register merges that would wait for them early.
+    uint32_t exr[P][B], esr[P];
+    auto gather = [&]() {
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            asm volatile("" : "+v"(ecol[p]), "+v"(eval[p]));
+            esr[p] = __float_as_uint(a.step[ecol[p]]);
+#pragma unroll
+            for (int b = 0; b < B; b++)
+                exr[p][b] = load_x_bits(a.x, (int64_t)b * a.cols + ecol[p], XBF16);
+        }
+    };
+
     {
         Lanes<S> L;
         init_lanes<S>(L, tab, raw, st0, off0);
         for (int k0 = 0; k0 < nk; k0 += KU) {
-            float xv[KU][S][B];
-#pragma unroll
-            for (int u = 0; u < KU; u++)
-#pragma unroll
-                for (int s = 0; s < S; s++) {
-                    // pin the use of the prefetched registers here (top of the
-                    // block) so the multiply is not hoisted next to the loads
-                    asm volatile("" : "+v"(sr[u][s]));
-#pragma unroll
-                    for (int b = 0; b < B; b++) {
-                        asm volatile("" : "+v"(xr[u][s][b]));
-                        xv[u][s][b] = bits_to_x(xr[u][s][b], XBF16) * sr[u][s];
-                    }
-                }
-            if (k0 + KU < nk) load_block(k0 + KU);
+            const bool more = k0 + KU < nk;
+            convert();
+            if (more) load_block(k0 + KU);
+            if (k0 == 0) gather();
             // keep the prefetch here: without this the scheduler sinks the
             // loads below the decode and the next block waits on them
             asm volatile("" ::: "memory");
@@ -359,7 +416,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
 #pragma unroll
                     for (int s = 0; s < S; s++) {
                         const float code =
-                        (float)rans_step<REFILL>(L.st[s], L.a[s], L.w[s], L.e[s], tab);
+                            (float)rans_step<REFILL>(L.st[s], L.a[s], L.w[s], L.e[s], tab);
 #pragma unroll
                         for (int b = 0; b < B; b++)
                             acc[r][b] = fmaf(code, xv[u][s][b], acc[r][b]);
@@ -369,29 +426,29 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         }
     }
 
-    // Escapes of this tile row (added once, by column group 0): wave w takes
-    // rows r = w, w+W, ..., its lanes stride over the row's side-table entries.
-    if (g == 0) {
-        for (int r = wave; r < R; r += W) {
-            const int e0 = __builtin_amdgcn_readlane(rp, r);
-            const int e1 = __builtin_amdgcn_readlane(rp, r + 1);
-            if (e0 == e1) continue;
-            float es[B];
+    float ev[B];
 #pragma unroll
-            for (int b = 0; b < B; b++) es[b] = 0.f;
-            for (int e = e0 + lane; e < e1; e += 64) {
-                const int col = a.esc_col[e];
-                const float v = (float)a.esc_val[e] * a.step[col];
+    for (int p = 0; p < P; p++) {
+        const int e = e_lo + 64 * (wave + p * W) + lane;
+        if (e_lo + 64 * (wave + p * W) < e_hi) {
+            asm volatile("" : "+v"(esr[p]));
 #pragma unroll
-                for (int b = 0; b < B; b++)
-                    es[b] = fmaf(v, load_x(a.x, (int64_t)b * a.cols + col, XBF16), es[b]);
-            }
+            for (int b = 0; b < B; b++) asm volatile("" : "+v"(exr[p][b]));
+            const float ve = e < e_hi ? (float)eval[p] * __uint_as_float(esr[p]) : 0.f;
 #pragma unroll
-            for (int b = 0; b < B; b++) {
-                const float v = wave_sum63(es[b]);
-                if (lane == 63) esc_red[r * B + b] = v;
-            }
+            for (int b = 0; b < B; b++) ev[b] = ve * bits_to_x(exr[p][b], XBF16);
+            add_escape<R, B>(acc, rp, e, ev);
         }
+    }
+    // further chunks (tile rows with more than 64*P*W escapes)
+    for (int e0 = e_lo + 64 * (wave + P * W); e0 < e_hi; e0 += 64 * W) {
+        const int e = e0 + lane;
+        const int ec = min(e, e_hi - 1);
+        const int col = a.esc_col[ec];
+        const float ve = e < e_hi ? (float)a.esc_val[ec] * a.step[col] : 0.f;
+#pragma unroll
+        for (int b = 0; b < B; b++) ev[b] = ve * load_x(a.x, (int64_t)b * a.cols + col, XBF16);
+        add_escape<R, B>(acc, rp, e, ev);
     }
 
 #pragma unroll
@@ -412,7 +469,6 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         b = tid - r * B;
         row = rb * R + r;
         for (int ww = 0; ww < W; ww++) v += red[ww * (R * B) + tid];
-        v += esc_red[tid];
     }
     if (a.ngroups == 1) {
         if (tid < R * B) a.y[(int64_t)b * a.rows + row] = v;
