@@ -91,6 +91,9 @@ struct DecodeArgs {
     const uint16_t* soffs;
     const uint32_t* states;
     const uint4* table_lds;
+    const int32_t* esc_rowptr;
+    const int32_t* esc_col;
+    const int32_t* esc_val;
     const float* step;
     void* out;
     int rows, cols, C, ncb, ntiles;
@@ -507,36 +510,58 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     }
 }
 
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-    const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu))  // NaN stays NaN
-        return (uint16_t)((u >> 16) | 0x40u);
-    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-}
+// bf16 of f, round to nearest even (gfx950's v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint16_t to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // Decode only.  MODE 0 writes int32 codes, MODE 1 writes bf16(code*step[c]).
-// One wave per tile; escapes are written afterwards by scatter_escapes.
+// One wave per tile, the staging and decode step of the GEMV.  Output goes
+// through one buffer resource over the tile row's R output rows: a store's
+// row is its scalar offset, its column step an immediate.  After its own
+// stores have completed, each wave overwrites the escape positions of its
+// tile (decoded as 0) with their side-table values, so no second launch.
 template <int R, int S, int MODE>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeArgs a) {
     __shared__ __align__(16) TabEntry tab[kProbM];
     extern __shared__ __align__(16) uint16_t dyn[];
     constexpr int nst = 64 * S;
+    constexpr int ESZ = MODE == 0 ? 4 : 2;
+    constexpr int KU = S >= 4 ? 2 : 4;
     const int W = a.W;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar tile math
     const int lane = threadIdx.x & 63;
     uint16_t* raw = dyn + (size_t)wave * a.L.wave_words;
     const int t = blockIdx.x * W + wave;
     const bool active = t < a.ntiles;
+    const int tc = active ? t : a.ntiles - 1;
+    const int rb = tc / a.ncb, cb = tc - rb * a.ncb;
+    asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.soffs), "s"(a.table_lds),
+                 "s"(a.words), "s"(a.step), "s"(a.esc_rowptr), "s"(a.out), "s"(a.C),
+                 "s"(a.cols), "s"(a.L.raw_words), "s"(a.W), "s"(a.ncb), "s"(a.ntiles));
 
-    const TileOff to = load_tile_off(a.tile_off, active ? t : a.ntiles - 1);
+    const TileOff to = load_tile_off(a.tile_off, tc);
+    const int rp = a.esc_rowptr[rb * R + min(lane, R)];
+    asm volatile("" ::: "memory");  // keep these two loads first
     uint32_t st0[S], off0[S];
-    if (active) {
 #pragma unroll
-        for (int s = 0; s < S; s++) {
-            st0[s] = a.states[t * nst + 64 * s + lane];
-            off0[s] = a.soffs[t * nst + 64 * s + lane];
-        }
+    for (int s = 0; s < S; s++) {
+        st0[s] = a.states[tc * nst + 64 * s + lane];
+        off0[s] = a.soffs[tc * nst + 64 * s + lane];
     }
+    const int nk = a.C / nst;
+    const int colbase = cb * a.C + lane;
+    const __amdgpu_buffer_rsrc_t srs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.step), 0, a.cols * 4, kBufWord3);
+    float sr[KU][S];
+    auto load_steps = [&](int k0) {
+        const int c0 = colbase + 64 * S * k0;
+#pragma unroll
+        for (int u = 0; u < KU; u++)
+#pragma unroll
+            for (int s = 0; s < S; s++)
+                sr[u][s] = __uint_as_float(
+                    __builtin_amdgcn_raw_buffer_load_b32(srs, (c0 + 64 * (S * u + s)) * 4, 0, 0));
+    };
+    if (MODE == 1) load_steps(0);
     uint32_t o0, n16;
     tile_extent(to, active, a.L.raw_words, o0, n16);
     stage_tile(raw, a.words, o0, n16, lane);
@@ -544,47 +569,63 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
     wait_vm();
     __syncthreads();
     if (!active) return;
+
+    uint8_t* obase = static_cast<uint8_t*>(a.out) + (size_t)rb * R * a.cols * ESZ;
+    const __amdgpu_buffer_rsrc_t ors =
+        __builtin_amdgcn_make_buffer_rsrc(obase, 0, R * a.cols * ESZ, kBufWord3);
     Lanes<S> L;
     init_lanes<S>(L, tab, raw, st0, off0);
-
-    const int rb = t / a.ncb, cb = t - rb * a.ncb;
-    const int nk = a.C / nst;
-    const int colbase = cb * a.C + lane;
-    for (int k = 0; k < nk; k++) {
-        // Symbol order within a state is k-major, r-minor; the S states of a
-        // lane advance together per row, as in the GEMV.
+    for (int k0 = 0; k0 < nk; k0 += KU) {
+        float sv[KU][S];
+        if (MODE == 1) {
 #pragma unroll
-        for (int r = 0; r < R; r++) {
+            for (int u = 0; u < KU; u++)
 #pragma unroll
-            for (int s = 0; s < S; s++) {
-                const int col = colbase + 64 * (S * k + s);
-                const int32_t code = rans_step<(R >= 8)>(L.st[s], L.a[s], L.w[s], L.e[s], tab);
-                const int64_t o = ((int64_t)rb * R + r) * a.cols + col;
-                if (MODE == 0)
-                    reinterpret_cast<int32_t*>(a.out)[o] = code;
-                else
-                    reinterpret_cast<uint16_t*>(a.out)[o] =
-                        f32_to_bf16_rne((float)code * a.step[col]);
+                for (int s = 0; s < S; s++) {
+                    asm volatile("" : "+v"(sr[u][s]));
+                    sv[u][s] = sr[u][s];
+                }
+            if (k0 + KU < nk) load_steps(k0 + KU);
+            asm volatile("" ::: "memory");
+        }
+        const int vb = (colbase + 64 * S * k0) * ESZ;
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            if (k0 + u >= nk) break;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+#pragma unroll
+                for (int s = 0; s < S; s++) {
+                    // symbol order within a state is k-major, r-minor, as in the GEMV
+                    const int32_t code = rans_step<(R >= 8)>(L.st[s], L.a[s], L.w[s], L.e[s], tab);
+                    const int vo = vb + 64 * (S * u + s) * ESZ;
+                    if (MODE == 0)
+                        __builtin_amdgcn_raw_buffer_store_b32(code, ors, vo, r * a.cols * 4, 0);
+                    else
+                        __builtin_amdgcn_raw_buffer_store_b16(to_bf16((float)code * sv[u][s]), ors,
+                                                              vo, r * a.cols * 2, 0);
+                }
             }
         }
     }
-}
 
-template <int MODE>
-__global__ void scatter_escapes_kernel(const int32_t* __restrict__ rowptr,
-                                       const int32_t* __restrict__ ecol,
-                                       const int32_t* __restrict__ eval,
-                                       const float* __restrict__ step, void* out, int rows,
-                                       int cols) {
-    const int row = blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= rows) return;
-    for (int e = rowptr[row]; e < rowptr[row + 1]; e++) {
-        const int col = ecol[e];
-        const int64_t o = (int64_t)row * cols + col;
-        if (MODE == 0)
-            reinterpret_cast<int32_t*>(out)[o] = eval[e];
-        else
-            reinterpret_cast<uint16_t*>(out)[o] = f32_to_bf16_rne((float)eval[e] * step[col]);
+    // Escapes of this tile: side-table entries of its rows whose column lies
+    // in [cb*C, cb*C + C).  The wave's own stores complete first, so the
+    // value lands after the 0 its position was decoded as.
+    wait_vm();
+    const int cmin = cb * a.C, cmax = cmin + a.C;
+    for (int r = 0; r < R; r++) {
+        const int e0 = __builtin_amdgcn_readlane(rp, r), e1 = __builtin_amdgcn_readlane(rp, r + 1);
+        for (int e = e0 + lane; e < e1; e += 64) {
+            const int col = a.esc_col[e];
+            if (col < cmin || col >= cmax) continue;
+            const int32_t v = a.esc_val[e];
+            if (MODE == 0)
+                __builtin_amdgcn_raw_buffer_store_b32(v, ors, col * 4, r * a.cols * 4, 0);
+            else
+                __builtin_amdgcn_raw_buffer_store_b16(to_bf16((float)v * a.step[col]), ors, col * 2,
+                                                      r * a.cols * 2, 0);
+        }
     }
 }
 
@@ -627,6 +668,12 @@ WaveLayout wave_layout(const rans_w64_matrix* m) {
 // Dynamic LDS bytes of a launch (the static arrays come on top).
 size_t lds_bytes(int waves, const WaveLayout& L) { return (size_t)waves * L.wave_words * 2; }
 
+// Largest byte extent a kernel addresses through one buffer resource
+// (an R-row slice of a decoded int32 output): it must fit the 32-bit range.
+bool fits_buffer_ranges(const rans_w64_matrix* m) {
+    return (int64_t)m->R * m->cols * 4 <= (int64_t)INT32_MAX;
+}
+
 bool valid_geometry(const rans_w64_matrix* m) {
     if (!m || (m->flags & ~RANS_F_WORDS_MASK) || (m->flags & RANS_F_WORDS_MASK) == RANS_F_WORDS_MASK)
         return false;
@@ -634,7 +681,7 @@ bool valid_geometry(const rans_w64_matrix* m) {
     if (m->rows % m->R || m->cols % m->C || m->C % (64 * m->S)) return false;
     if (m->max_tile_words <= 0 || m->max_tile_words > 65536) return false;
     if (m->max_state_words <= 0 || m->max_state_words > m->max_tile_words) return false;
-    return true;
+    return fits_buffer_ranges(m);
 }
 
 bool valid_pointers(const rans_w64_matrix* m) {
@@ -771,6 +818,9 @@ int launch_decode_common(const rans_w64_matrix* m, void* out, hipStream_t stream
     a.soffs = m->soffs;
     a.states = m->states;
     a.table_lds = reinterpret_cast<const uint4*>(m->table_lds);
+    a.esc_rowptr = m->esc_rowptr;
+    a.esc_col = m->esc_col;
+    a.esc_val = m->esc_val;
     a.step = m->step;
     a.out = out;
     a.rows = m->rows;
@@ -781,12 +831,7 @@ int launch_decode_common(const rans_w64_matrix* m, void* out, hipStream_t stream
     a.W = waves;
     a.L = wave_layout(m);
     const int grid = (a.ntiles + waves - 1) / waves;
-    int rc = dispatch_decode<MODE>(a, m->R, m->S, waves, lds_bytes(waves, a.L), grid, stream);
-    if (rc != 0) return rc;
-    hipLaunchKernelGGL((scatter_escapes_kernel<MODE>), dim3((m->rows + 255) / 256), dim3(256), 0,
-                       stream, m->esc_rowptr, m->esc_col, m->esc_val, m->step, out, m->rows,
-                       m->cols);
-    return (int)hipGetLastError();
+    return dispatch_decode<MODE>(a, m->R, m->S, waves, lds_bytes(waves, a.L), grid, stream);
 }
 
 }  // namespace
