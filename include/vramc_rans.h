@@ -62,12 +62,14 @@ extern "C" {
 #define RANS_ECODES (-5)       /* encoder: degenerate or empty symbol distribution */
 #define RANS_ETILE (-6)        /* encoder: a tile block exceeds 65535 words */
 
-/* rans_w64_matrix.flags: how the GEMV fetches renormalisation words.  The
- * decoded values are identical; only speed differs.  0 = library default
- * (REFILL for R >= 8, ALWAYS otherwise). */
+/* rans_w64_matrix.flags.  Word fetch (bits 0-1): how the GEMV fetches
+ * renormalisation words; the decoded values are identical, only speed
+ * differs; 0 = library default (REFILL for R >= 8, ALWAYS otherwise). */
 #define RANS_F_WORDS_ALWAYS 1 /* every lane re-reads its next word each step */
 #define RANS_F_WORDS_REFILL 2 /* only lanes that consumed their word fetch the next */
 #define RANS_F_WORDS_MASK 3
+#define RANS_F_NO_ESCAPES 4   /* the side table is empty: kernels skip it (a promise; a
+                                 matrix with escapes decodes them as 0 under this flag) */
 
 typedef struct rans_w64_matrix {
     int32_t rows, cols;       /* out_features, in_features */

@@ -45,8 +45,8 @@ def test_argument_validation_without_gpu(rans, lib):
     assert lib.launch_rans_gemv(None, x, 0, 1, y, None) == -2
     bad = _desc(rans, cols=4000)
     assert lib.launch_rans_gemv(ctypes.byref(bad), x, 0, 1, y, None) == -2
-    r3 = _desc(rans, rows=255, R=3)
-    assert lib.launch_rans_gemv(ctypes.byref(r3), x, 0, 1, y, None) == -1
+    r5 = _desc(rans, rows=255, R=5)  # no kernel compiled for R=5
+    assert lib.launch_rans_gemv(ctypes.byref(r5), x, 0, 1, y, None) == -1
     assert lib.launch_rans_gemv(ctypes.byref(d), x, 7, 1, y, None) == -4
     assert lib.launch_rans_gemv(ctypes.byref(d), None, 0, 1, y, None) == -4
     assert lib.launch_rans_gemv(ctypes.byref(d), x, 0, 0, y, None) == -4
@@ -59,7 +59,7 @@ def test_argument_validation_without_gpu(rans, lib):
     assert lib.rans_gemv_workspace_bytes(ctypes.byref(one), 1) == 0
     huge = _desc(rans, mtw=70000)
     assert lib.rans_gemv_workspace_bytes(ctypes.byref(huge), 1) == -2
-    for flags in (3, 4, -1):  # both word-fetch bits, or an unknown bit
+    for flags in (3, 8, -1):  # both word-fetch bits, or an unknown bit
         bad_flags = _desc(rans, cols=2048)
         bad_flags.flags = flags
         assert lib.launch_rans_gemv(ctypes.byref(bad_flags), x, 0, 1, y, None) == -2

@@ -293,3 +293,21 @@ def test_full_size_27b_shapes(rans, oracle, lib, dev, rows, cols):
     assert torch.equal(m.gemv(x).cpu(), y4)
     assert _rel_l2(y4.numpy(), ref) <= REL_L2
     assert _rel_l2(y1.numpy(), ref[0]) <= REL_L2
+
+
+def test_no_escape_flag(rans, oracle, lib, dev):
+    """A matrix without escapes gets RANS_F_NO_ESCAPES from the wrapper; the
+    kernels then skip the side table.  Same outputs, bit for bit, as with
+    the side table walked (flag cleared)."""
+    print("case no-escape flag", flush=True)
+    codes = oracle.synth_codes(384, 2048, 3.25, seed=21)
+    step = (np.random.default_rng(3).random(2048) + 0.5).astype(np.float32)
+    enc = rans.encode(codes, 8, 512, 1)
+    m = rans.RansMatrix(enc, torch.from_numpy(step), lib)
+    assert m.flags & rans.F_NO_ESCAPES
+    x = torch.randn(4, 2048, device="cuda").bfloat16()
+    y_skip, d_skip = m.gemv(x).cpu(), m.decode().cpu()
+    m._desc.flags = m.flags & ~rans.F_NO_ESCAPES
+    assert torch.equal(m.gemv(x).cpu(), y_skip)
+    assert torch.equal(m.decode().cpu(), d_skip)
+    np.testing.assert_array_equal(m.decode_codes().cpu().numpy(), codes)

@@ -81,7 +81,8 @@ struct GemvArgs {
     float* partial;      // [ngroups][B][rows]
     uint32_t* counters;  // [rows/R]
     int rows, cols, C, ncb, ngroups;
-    int W;  // waves per workgroup (= blockDim.x / 64, as a kernel argument)
+    int W;        // waves per workgroup (= blockDim.x / 64, as a kernel argument)
+    int has_esc;  // 0: the side table is empty
     WaveLayout L;
 };
 
@@ -97,7 +98,8 @@ struct DecodeArgs {
     const float* step;
     void* out;
     int rows, cols, C, ncb, ntiles;
-    int W;  // waves per workgroup
+    int W;        // waves per workgroup
+    int has_esc;  // 0: the side table is empty
     WaveLayout L;
 };
 
@@ -305,7 +307,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     // buffer loads ranged to one x row / the step vector: a block's columns
     // are immediate offsets on one base register, and columns past the end
     // of the matrix (the tail of the last block) read as 0.
-    constexpr int KU = S >= 4 ? 2 : 4;  // 8 (column, state) groups in flight at S=2 and S=4
+    // column steps per prefetch block: 4, or 2 where the prefetch registers
+    // would otherwise cost occupancy (S=4, or a batch of 4)
+    constexpr int KU = (S >= 4 || B >= 4) ? 2 : 4;
     constexpr int XS = XBF16 ? 2 : 4;
     __amdgpu_buffer_rsrc_t xrs[B];
 #pragma unroll
@@ -343,8 +347,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     // it costs nothing more), and its x and step gathers go out before the
     // decode loop, their values kept raw until after the loop, so that
     // latency overlaps the decode.
-    const int e_lo = g == 0 ? __builtin_amdgcn_readlane(rp, 0) : 0;
-    const int e_hi = g == 0 ? __builtin_amdgcn_readlane(rp, R) : 0;
+    const bool esc = a.has_esc && g == 0;  // kernel-uniform
+    const int e_lo = esc ? __builtin_amdgcn_readlane(rp, 0) : 0;
+    const int e_hi = esc ? __builtin_amdgcn_readlane(rp, R) : 0;
     asm volatile("" ::"s"(e_lo), "s"(e_hi));
     stage_tile(raw, a.words, o0, n16, lane);
     stage_table(tab, a.table_lds, wave, W, lane);
@@ -407,7 +412,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
             const bool more = k0 + KU < nk;
             convert();
             if (more) load_block(k0 + KU);
-            if (k0 == 0) gather();
+            if (k0 == 0 && esc) gather();
             // keep the prefetch here: without this the scheduler sinks the
             // loads below the decode and the next block waits on them
             asm volatile("" ::: "memory");
@@ -612,6 +617,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
     // Escapes of this tile: side-table entries of its rows whose column lies
     // in [cb*C, cb*C + C).  The wave's own stores complete first, so the
     // value lands after the 0 its position was decoded as.
+    if (!a.has_esc) return;
     wait_vm();
     const int cmin = cb * a.C, cmax = cmin + a.C;
     for (int r = 0; r < R; r++) {
@@ -675,7 +681,8 @@ bool fits_buffer_ranges(const rans_w64_matrix* m) {
 }
 
 bool valid_geometry(const rans_w64_matrix* m) {
-    if (!m || (m->flags & ~RANS_F_WORDS_MASK) || (m->flags & RANS_F_WORDS_MASK) == RANS_F_WORDS_MASK)
+    if (!m || (m->flags & ~(RANS_F_WORDS_MASK | RANS_F_NO_ESCAPES)) ||
+        (m->flags & RANS_F_WORDS_MASK) == RANS_F_WORDS_MASK)
         return false;
     if (m->rows <= 0 || m->cols <= 0 || m->R <= 0 || m->C <= 0 || m->S <= 0) return false;
     if (m->rows % m->R || m->cols % m->C || m->C % (64 * m->S)) return false;
@@ -772,6 +779,7 @@ int dispatch_gemv(const GemvArgs& a, int R, int S, int B, int var, int waves, si
     switch (R) {
         case 1: return dispatch_s<1>(a, S, B, var, waves, lds, grid, st);
         case 2: return dispatch_s<2>(a, S, B, var, waves, lds, grid, st);
+        case 3: return dispatch_s<3>(a, S, B, var, waves, lds, grid, st);
         case 4: return dispatch_s<4>(a, S, B, var, waves, lds, grid, st);
         case 8: return dispatch_s<8>(a, S, B, var, waves, lds, grid, st);
         case 16: return dispatch_s<16>(a, S, B, var, waves, lds, grid, st);
@@ -780,7 +788,7 @@ int dispatch_gemv(const GemvArgs& a, int R, int S, int B, int var, int waves, si
 }
 
 bool supported_rs(int R, int S) {
-    return (R == 1 || R == 2 || R == 4 || R == 8 || R == 16) && (S == 1 || S == 2 || S == 4);
+    return (R == 1 || R == 2 || R == 3 || R == 4 || R == 8 || R == 16) && (S == 1 || S == 2 || S == 4);
 }
 
 template <int R, int S, int MODE>
@@ -799,7 +807,7 @@ int dispatch_decode(const DecodeArgs& a, int R, int S, int waves, size_t lds, in
 #define VRAMC_DEC_CASE(RR, SS) \
     if (R == RR && S == SS) return launch_decode_t<RR, SS, MODE>(a, waves, lds, grid, st);
 #define VRAMC_DEC_R(RR) VRAMC_DEC_CASE(RR, 1) VRAMC_DEC_CASE(RR, 2) VRAMC_DEC_CASE(RR, 4)
-    VRAMC_DEC_R(1) VRAMC_DEC_R(2) VRAMC_DEC_R(4) VRAMC_DEC_R(8) VRAMC_DEC_R(16)
+    VRAMC_DEC_R(1) VRAMC_DEC_R(2) VRAMC_DEC_R(3) VRAMC_DEC_R(4) VRAMC_DEC_R(8) VRAMC_DEC_R(16)
 #undef VRAMC_DEC_R
 #undef VRAMC_DEC_CASE
     return RANS_EUNSUPPORTED;
@@ -829,6 +837,7 @@ int launch_decode_common(const rans_w64_matrix* m, void* out, hipStream_t stream
     a.ncb = m->cols / m->C;
     a.ntiles = (m->rows / m->R) * a.ncb;
     a.W = waves;
+    a.has_esc = !(m->flags & RANS_F_NO_ESCAPES);
     a.L = wave_layout(m);
     const int grid = (a.ntiles + waves - 1) / waves;
     return dispatch_decode<MODE>(a, m->R, m->S, waves, lds_bytes(waves, a.L), grid, stream);
@@ -880,6 +889,7 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
     a.ncb = ncb;
     a.ngroups = ngroups;
     a.W = waves;
+    a.has_esc = !(m->flags & RANS_F_NO_ESCAPES);
     a.L = wave_layout(m);
     a.counters = ngroups > 1 ? static_cast<uint32_t*>(m->workspace) : nullptr;
     a.partial = ngroups > 1

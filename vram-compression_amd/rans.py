@@ -35,8 +35,9 @@ ESC = 0  # escape symbol: codes outside [-127, 127]
 LANES = 64
 
 X_F32, X_BF16 = 0, 1
-# rans_w64_matrix.flags: word fetch of the GEMV (0 = library default)
-F_WORDS_ALWAYS, F_WORDS_REFILL = 1, 2
+# rans_w64_matrix.flags: word fetch of the GEMV (0 = library default), and
+# the empty-side-table promise (set by RansMatrix itself)
+F_WORDS_ALWAYS, F_WORDS_REFILL, F_WORDS_MASK, F_NO_ESCAPES = 1, 2, 3, 4
 
 HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared",
                # packed fp32 VALU ops stay disabled on this platform
@@ -220,13 +221,14 @@ def encode(codes, R, C, S=1, threads=None):
 
 def pick_tiling(rows, cols, R=None, S=1, target_states=None):
     """A legal (R, C) for the w64 format: C a multiple of 64*S dividing cols,
-    R in {1, 2, 4, 8, 16}.  Chosen by measurement on MI355X:
+    R in {1, 2, 3, 4, 8, 16}.  Chosen by measurement on MI355X:
 
-    - states: about 140 symbols per state for mid-size matrices (~98K
-      states); small ones get more states, down to 64 symbols each, so the
-      chip has about one wavefront per SIMD; matrices above 32M weights use
-      about 160 symbols per state.  Fewer states cost less per-state
-      overhead (48 bits each), more states give more parallelism.
+    - states: about 105 symbols per state for mid-size matrices (at
+      1536x8960 that is 2048 waves, two per SIMD: two waves on a SIMD slow
+      each other by only ~15%, so a one-wave SIMD is mostly idle capacity);
+      small ones get more states, down to 64 symbols each; matrices above
+      32M weights use about 160 symbols per state.  Fewer states cost less
+      per-state overhead (48 bits each), more states give more parallelism.
     - column tiles per tile row (ncb): 8 is best (8 waves of a workgroup
       share one LDS table, so more waves fit per CU), then 4-7 and 16 (the
       latter needs the split-K reduction); fewer than 4 repeat the table
@@ -234,14 +236,14 @@ def pick_tiling(rows, cols, R=None, S=1, target_states=None):
     nst = 64 * S
     cands = [c for c in range(nst, cols + 1, nst) if cols % c == 0]
     assert cands, f"cols={cols} has no divisor that is a multiple of {nst}"
-    Rs = [R] if R else [r for r in (16, 8, 4, 2, 1) if rows % r == 0]
+    Rs = [R] if R else [r for r in (16, 8, 4, 3, 2, 1) if rows % r == 0]
     n = rows * cols
     if target_states:
         target = target_states
     elif n >= (32 << 20):
         target = n // 160
     else:
-        target = int(min(max(n // 140, min(98304, n // 64)), 262144))
+        target = int(min(max(n // 105, min(98304, n // 64)), 262144))
     best = None
     for r in Rs:
         for c in cands:
@@ -300,7 +302,8 @@ class RansMatrix:
 
     def __init__(self, enc, step, lib, flags=0):
         """flags: F_WORDS_ALWAYS / F_WORDS_REFILL picks the GEMV's word
-        fetch (same results, different speed); 0 lets the library choose."""
+        fetch (same results, different speed); 0 lets the library choose.
+        F_NO_ESCAPES is added here when the matrix has no escapes."""
         _require_gpu()
         if lib is None:
             raise RuntimeError("librans_hip.so not loaded")
@@ -334,7 +337,8 @@ class RansMatrix:
         self._desc = RansMatrixDesc(
             rows=self.rows, cols=self.cols, R=self.R, C=self.C, S=self.S,
             max_tile_words=self.max_tile_words, max_state_words=self.max_state_words,
-            flags=int(flags), words=self.words.data_ptr(), tile_off=self.tile_off.data_ptr(),
+            flags=(int(flags) & F_WORDS_MASK) | (0 if len(enc["esc_col"]) else F_NO_ESCAPES),
+            words=self.words.data_ptr(), tile_off=self.tile_off.data_ptr(),
             soffs=self.soffs.data_ptr(), states=self.states.data_ptr(),
             table=None, table_lds=self.table_lds.data_ptr(),
             esc_rowptr=self.esc_rowptr.data_ptr(),
@@ -357,8 +361,9 @@ class RansMatrix:
         x = torch.randn(batch, self.cols, device="cuda").to(x_dtype)
         y = torch.empty(batch, self.rows, device="cuda")
         best = None
+        keep = self._desc.flags & ~F_WORDS_MASK
         for f in (F_WORDS_ALWAYS, F_WORDS_REFILL):
-            self._desc.flags = f
+            self._desc.flags = f | keep
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):
@@ -381,7 +386,7 @@ class RansMatrix:
             del g
             if best is None or t < best[0]:
                 best = (t, f)
-        self._desc.flags = best[1]
+        self._desc.flags = best[1] | keep
         return best[1]
 
     @property

@@ -254,11 +254,11 @@ def qwen15b_layer_shapes():
 
 
 def chain_tiling(rows, cols):
-    """Tiling for one matrix of the per-token chain: about 140 symbols per
+    """Tiling for one matrix of the per-token chain: about 105 symbols per
     state on large matrices, fewer on small ones (whose decode would
     otherwise be latency-bound far above their byte count)."""
     n = rows * cols
-    target = max(n // 140, min(n // 35, 49152))
+    target = max(n // 105, min(n // 35, 49152))
     return pick_tiling(rows, cols, S=1, target_states=target)
 
 
@@ -286,7 +286,7 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
     got = ms[0].gemv(x)
     err = float((got - ref).norm() / ref.norm())
     out = dict(rows=rows, cols=cols, bits_target=bits, dist=dist, escape_frac=escape_frac,
-               batch=batch, R=R, C=C, S=S, word_fetch={1: "always", 2: "refill"}[flags],
+               batch=batch, R=R, C=C, S=S, word_fetch={1: "always", 2: "refill"}[flags & 3],
                entropy=entropy_fast(codes),
                bits_total=8 * m.nbytes / codes.size, n_escapes=int(len(enc["esc_col"])),
                t_rans_us=t_rans, t_bf16_us=t_bf16,
