@@ -27,6 +27,7 @@
 
 #include <cstdint>
 #include <mutex>
+#include <type_traits>
 
 #include "../../include/vramc_rans.h"
 
@@ -168,6 +169,17 @@ __device__ __forceinline__ uint32_t load_x_bits(const void* x, int64_t i, bool b
 __device__ __forceinline__ float bits_to_x(uint32_t v, bool bf16) {
     return __uint_as_float(bf16 ? v << 16 : v);
 }
+
+template <typename T>
+__device__ __forceinline__ T raw_load(__amdgpu_buffer_rsrc_t r, int off) {
+    if constexpr (std::is_same_v<T, __bf16>)
+        return __builtin_bit_cast(__bf16, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+    else
+        return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+__device__ __forceinline__ float raw_to_x(__bf16 v) { return (float)v; }
+__device__ __forceinline__ float raw_to_x(uint32_t v) { return __uint_as_float(v); }
 
 __device__ __forceinline__ float load_x(const void* x, int64_t i, bool bf16) {
     return bits_to_x(load_x_bits(x, i, bf16), bf16);
@@ -319,7 +331,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
             a.cols * XS, kBufWord3);
     const __amdgpu_buffer_rsrc_t srs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.step), 0, a.cols * 4, kBufWord3);
-    uint32_t xr[KU][S][B];  // raw bits: bf16 zero-extended, or f32
+    // bf16 values kept as __bf16 (an integer register pin would be widened
+    // first, at the cost of a mask per value), or f32 bits
+    using XRaw = std::conditional_t<XBF16, __bf16, uint32_t>;
+    XRaw xr[KU][S][B];
     float sr[KU][S];
     auto load_block = [&](int k0) {
         const int c0 = colbase + 64 * S * k0;
@@ -332,8 +347,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
 #pragma unroll
                 for (int b = 0; b < B; b++)
                     xr[u][s][b] =
-                        XBF16 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(xrs[b], c * 2, 0, 0)
-                              : __builtin_amdgcn_raw_buffer_load_b32(xrs[b], c * 4, 0, 0);
+                        raw_load<XRaw>(xrs[b], XBF16 ? c * 2 : c * 4);
             }
         }
     };
@@ -385,7 +399,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
 #pragma unroll
                 for (int b = 0; b < B; b++) {
                     asm volatile("" : "+v"(xr[u][s][b]));
-                    xv[u][s][b] = bits_to_x(xr[u][s][b], XBF16) * sr[u][s];
+                    xv[u][s][b] = raw_to_x(xr[u][s][b]) * sr[u][s];
+                    // all multiplies here, so the prefetch that follows can
+                    // overwrite sr and xr without copies
+                    asm volatile("" : "+v"(xv[u][s][b]));
                 }
             }
     };
@@ -409,9 +426,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         Lanes<S> L;
         init_lanes<S>(L, tab, raw, st0, off0);
         for (int k0 = 0; k0 < nk; k0 += KU) {
-            const bool more = k0 + KU < nk;
             convert();
-            if (more) load_block(k0 + KU);
+            // unconditional: past the last block these read columns of the
+            // next tile, or 0 past the end of the matrix, and go unused; a
+            // conditional prefetch makes the compiler copy the registers
+            load_block(k0 + KU);
             if (k0 == 0 && esc) gather();
             // keep the prefetch here: without this the scheduler sinks the
             // loads below the decode and the next block waits on them
