@@ -203,6 +203,53 @@ __device__ __forceinline__ float wave_sum63(float v) {
     return v;
 }
 
+// Sums each of N values (a power of two up to 64) over the 64 lanes with
+// about 2.2*N instructions instead of 6*N.  Stage j (j = 0..5) pairs the
+// lanes that differ in lane-id bit 5-j.  While a lane holds n > 1 values it
+// keeps the half selected by that bit and adds its partner's copy of the
+// same half, so the value count halves; once n = 1 a stage is a plain pair
+// sum.  Partners: v_permlane32_swap / v_permlane16_swap exchange the halves
+// directly for bits 5 and 4; DPP row_mirror, row_half_mirror and quad_perm
+// reach them for bits 3..0 (a mirror pairs lanes differing in that bit, and
+// lanes that share the bits already summed hold disjoint lane sets).  Every
+// lane ends with the complete total of value index lane >> (6 - log2 N).
+template <int J, int N>
+__device__ __forceinline__ void wave_transpose_stage(float* w, int lane) {
+    if constexpr (J < 6) {
+        constexpr int bit = 5 - J;
+        constexpr int CTRL = J == 2 ? 0x140 : J == 3 ? 0x141 : J == 4 ? 0x4E : 0xB1;
+        constexpr int h = N > 1 ? N / 2 : 1;
+        const bool hi = (lane >> bit) & 1;
+#pragma unroll
+        for (int i = 0; i < h; i++) {
+            const float a = w[i], b = N > 1 ? w[i + h] : w[i];
+            if constexpr (J == 0) {
+                const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b),
+                                                                false, false);
+                w[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+            } else if constexpr (J == 1) {
+                const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b),
+                                                                false, false);
+                w[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+            } else if constexpr (N > 1) {
+                w[i] = (hi ? b : a) + dpp<CTRL>(hi ? a : b);
+            } else {
+                w[i] = a + dpp<CTRL>(a);
+            }
+        }
+        wave_transpose_stage<J + 1, h>(w, lane);
+    }
+}
+
+template <int N>
+__device__ __forceinline__ float wave_transpose_sum(float (&v)[N], int lane) {
+    static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N must be a power of two <= 64");
+    wave_transpose_stage<0, N>(v, lane);
+    return v[0];
+}
+
+constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
+
 // Per-lane decoder state of S interleaved rANS states, with the table entry
 // of each state's next symbol already read (software pipelined: the read for
 // symbol i+1 is issued before the GEMV work of symbol i).
@@ -268,10 +315,14 @@ __device__ __forceinline__ void add_escape(float (&acc)[R][B], int rp, int e, co
     int re = 0;
 #pragma unroll
     for (int r = 1; r < R; r++) re += e >= __builtin_amdgcn_readlane(rp, r) ? 1 : 0;
+    // a 0/1 weight per row and one FMA per (row, batch): 2R + RB
+    // instructions rather than R + 2RB for a select and an add
 #pragma unroll
-    for (int r = 0; r < R; r++)
+    for (int r = 0; r < R; r++) {
+        const float m = re == r ? 1.f : 0.f;
 #pragma unroll
-        for (int b = 0; b < B; b++) acc[r][b] += re == r ? v[b] : 0.f;
+        for (int b = 0; b < B; b++) acc[r][b] = fmaf(m, v[b], acc[r][b]);
+    }
 }
 
 template <int R, int S, int B, bool XBF16, bool REFILL>
@@ -445,8 +496,14 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
                         const float code =
                             (float)rans_step<REFILL>(L.st[s], L.a[s], L.w[s], L.e[s], tab);
 #pragma unroll
-                        for (int b = 0; b < B; b++)
+                        for (int b = 0; b < B; b++) {
                             acc[r][b] = fmaf(code, xv[u][s][b], acc[r][b]);
+                            // with the refill branches the compiler sinks
+                            // the conversions and FMAs to the end of the
+                            // block, keeping every step's 64-bit table entry
+                            // live; consuming the sum here keeps them in place
+                            if (REFILL) asm volatile("" : "+v"(acc[r][b]));
+                        }
                     }
                 }
             }
@@ -478,12 +535,24 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         add_escape<R, B>(acc, rp, e, ev);
     }
 
+    constexpr int NRB = R * B;
+    if constexpr (NRB >= 8 && (NRB & (NRB - 1)) == 0) {
+        float w[NRB];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
+        for (int r = 0; r < R; r++)
 #pragma unroll
-        for (int b = 0; b < B; b++) {
-            const float v = wave_sum63(acc[r][b]);
-            if (lane == 63) red[wave * (R * B) + r * B + b] = v;
+            for (int b = 0; b < B; b++) w[r * B + b] = acc[r][b];
+        const float v = wave_transpose_sum<NRB>(w, lane);
+        constexpr int sh = 6 - ilog2(NRB);
+        if ((lane & ((1 << sh) - 1)) == 0) red[wave * NRB + (lane >> sh)] = v;
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const float v = wave_sum63(acc[r][b]);
+                if (lane == 63) red[wave * NRB + r * B + b] = v;
+            }
         }
     }
     __syncthreads();
