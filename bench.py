@@ -57,8 +57,8 @@ def algorithmic_bytes(enc, rows, cols, batch=1):
     initial states, the 32 KB LDS image of the table, the escape side table),
     x (bf16), the step vector (f32) and y (f32)."""
     comp = (enc["words"].nbytes + enc["tile_off"].nbytes + enc["soffs"].nbytes +
-            enc["states"].nbytes + 2 * enc["table"].nbytes + enc["esc_rowptr"].nbytes +
-            enc["esc_col"].nbytes + enc["esc_val"].nbytes)
+            enc["states"].nbytes + 2 * enc["table"].nbytes + enc["esc_tileptr"].nbytes +
+            enc["esc_pos"].nbytes + enc["esc_val"].nbytes)
     return comp, comp + cols * 2 * batch + cols * 4 + rows * 4 * batch
 
 

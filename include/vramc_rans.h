@@ -30,8 +30,11 @@
  *     32-bit state, 16-bit renormalisation words, 12-bit probabilities,
  *     table[slot] = sym | freq<<8 | (slot-cum)<<20, sym = code + 128.
  *   - Symbol 0 is the escape: codes outside [-127, 127] are coded as symbol 0
- *     and their values live in a CSR side table (esc_rowptr/esc_col/esc_val,
- *     columns ascending within a row).
+ *     and their values live in a side table kept per tile: tile t's entries
+ *     are esc_pos/esc_val[esc_tileptr[t] .. esc_tileptr[t+1]), esc_pos =
+ *     (c << 8) | r for the code at tile row r, tile column c (row rb*R+r,
+ *     column cb*C+c), strictly ascending within the tile, so a tile's
+ *     entries run in column order (R <= 256).
  *   - words: all tile blocks concatenated; tile t's block is
  *     words[tile_off[t] .. tile_off[t+1]), a multiple of 8 words with at least
  *     one trailing pad word; state j's stream starts at tile_off[t]+soffs[t*64*S+j]
@@ -64,7 +67,7 @@ extern "C" {
 
 /* rans_w64_matrix.flags.  Word fetch (bits 0-1): how the GEMV fetches
  * renormalisation words; the decoded values are identical, only speed
- * differs; 0 = library default (REFILL for R >= 8, ALWAYS otherwise). */
+ * differs; 0 = library default (REFILL for R >= 3, ALWAYS otherwise). */
 #define RANS_F_WORDS_ALWAYS 1 /* every lane re-reads its next word each step */
 #define RANS_F_WORDS_REFILL 2 /* only lanes that consumed their word fetch the next */
 #define RANS_F_WORDS_MASK 3
@@ -85,8 +88,8 @@ typedef struct rans_w64_matrix {
     const uint32_t* table;    /* [4096], reference packing (host decoder) */
     const uint32_t* table_lds;/* [8192], the table as the kernels hold it in LDS, made
                                  by rans_table_lds from table (device kernels) */
-    const int32_t* esc_rowptr;/* [rows+1] */
-    const int32_t* esc_col;   /* [nesc] */
+    const int32_t* esc_tileptr;/* [ntiles+1] */
+    const int32_t* esc_pos;   /* [nesc], (tile column << 8) | tile row */
     const int32_t* esc_val;   /* [nesc] */
     const float* step;        /* [cols] per-column step (waterfilling) */
     void* workspace;          /* split-K partials + counters; zero-filled once */
@@ -140,7 +143,9 @@ int rans_build_table(const uint8_t* sym, int64_t n, int64_t* freq, int64_t* cum,
 int rans_table_lds(const uint32_t* table, uint32_t* out);
 
 /* Encode int32 codes (rows x cols, row-major) into the w64 format; replaces
- * encode() (rans.py:62-98).  On success *handle owns the result and info[]
+ * encode() (rans.py:62-98).  R <= 256 and C < 2^23 (the side table's
+ * position packing), else RANS_EGEOMETRY.  On success *handle owns the
+ * result and info[]
  * receives {nwords, ntiles, nstates, nesc, max_tile_words, payload_words,
  * max_state_words}.
  * Fetch the arrays with rans_w64_encode_fetch, then free the handle. */
@@ -149,7 +154,7 @@ int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols, int32_t R,
 
 int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off, uint16_t* soffs,
                           uint32_t* states, uint32_t* table, int64_t* freq,
-                          int32_t* esc_rowptr, int32_t* esc_col, int32_t* esc_val);
+                          int32_t* esc_tileptr, int32_t* esc_pos, int32_t* esc_val);
 
 void rans_w64_encode_free(void* handle);
 

@@ -280,15 +280,27 @@ def w64_decode(enc):
     sym = w64_unorder(out, rows, cols, R, C, S)
     codes = sym.astype(np.int64) - OFFSET
     esc_mask = sym == ESC
-    rp = enc["esc_rowptr"].astype(np.int64)
-    ecol = enc["esc_col"].astype(np.int64)
+    # side table per tile: tile t owns entries tp[t]..tp[t+1], each at tile
+    # row pos & 255, tile column pos >> 8, strictly ascending within the tile
+    tp = enc["esc_tileptr"].astype(np.int64)
+    pos = enc["esc_pos"].astype(np.int64)
     eval_ = enc["esc_val"].astype(np.int64)
-    er = np.repeat(np.arange(rows), np.diff(rp))
+    if tp.size != ntiles + 1 or tp[0] != 0 or np.any(np.diff(tp) < 0) or tp[-1] != pos.size:
+        raise AssertionError("escape tile pointers malformed")
+    t = np.repeat(np.arange(ntiles), np.diff(tp))
+    r, c = pos & 0xFF, pos >> 8
+    if np.any(pos < 0) or np.any(r >= R) or np.any(c >= C):
+        raise AssertionError("escape position outside its tile")
+    same = t[1:] == t[:-1]
+    if np.any(pos[1:][same] <= pos[:-1][same]):
+        raise AssertionError("escape positions not strictly ascending within a tile")
+    ncb = cols // C
+    er, ec = (t // ncb) * R + r, (t % ncb) * C + c
     flagged = np.zeros_like(esc_mask)
-    flagged[er, ecol] = True
+    flagged[er, ec] = True
     if not np.array_equal(flagged, esc_mask):
         raise AssertionError("escape side table disagrees with escape symbols in the stream")
-    codes[er, ecol] = eval_
+    codes[er, ec] = eval_
     return codes
 
 

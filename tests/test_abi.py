@@ -35,7 +35,7 @@ def _desc(rans, rows=256, cols=4096, R=8, C=256, S=1, mtw=1024):
                                max_state_words=64,
                                words=fake, tile_off=fake, soffs=fake, states=fake, table=fake,
                                table_lds=fake,
-                               esc_rowptr=fake, esc_col=fake, esc_val=fake, step=fake,
+                               esc_tileptr=fake, esc_pos=fake, esc_val=fake, step=fake,
                                workspace=None, workspace_bytes=0)
 
 

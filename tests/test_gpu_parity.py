@@ -89,7 +89,7 @@ def test_mlp_waterfill_escapes(rans, oracle, lib, dev, rows, cols):
     x = np.random.default_rng(3).standard_normal(cols).astype(np.float32)
     R, C = B.pick_tiling(rows, cols, S=1)
     m, enc = _check_matrix(rans, oracle, lib, codes, R, C, 1, step, [x], exact_bf16=False)
-    assert len(enc["esc_col"]) > 0
+    assert len(enc["esc_pos"]) > 0
     # bf16 decode including escapes
     dec = m.decode().cpu()
     want = (torch.from_numpy(codes.astype(np.float32)) * torch.from_numpy(step)).bfloat16()
@@ -311,3 +311,35 @@ def test_no_escape_flag(rans, oracle, lib, dev):
     assert torch.equal(m.gemv(x).cpu(), y_skip)
     assert torch.equal(m.decode().cpu(), d_skip)
     np.testing.assert_array_equal(m.decode_codes().cpu().numpy(), codes)
+
+
+@pytest.mark.parametrize("rows,cols,R,C", [(4096, 256, 2, 256), (2048, 512, 4, 256),
+                                           (1536, 768, 1, 256), (1536, 8960, 3, 2240)])
+def test_few_column_tiles(rans, oracle, lib, dev, rows, cols, R, C):
+    """Many tile rows of few column tiles (1, 2, 3 and 4 per row: one
+    workgroup of that many waves per tile row).  Escapes in several rows,
+    batch 1, 3 and 4, both word-fetch policies bitwise equal, GEMV against
+    the float64 oracle."""
+    print(f"case few column tiles {rows}x{cols} R={R} C={C}", flush=True)
+    codes = oracle.synth_codes(rows, cols, 3.0, seed=rows + C)
+    rng = np.random.default_rng(R)
+    hit = rng.random(codes.shape) < 0.002
+    codes[hit] = rng.integers(128, 700, size=int(hit.sum())) * rng.choice([-1, 1], int(hit.sum()))
+    step = (rng.random(cols) + 0.5).astype(np.float32)
+    enc = rans.encode(codes, R, C, 1)
+    x = torch.from_numpy(rng.standard_normal((4, cols)).astype(np.float32)).cuda().bfloat16()
+    ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64), step.astype(np.float64))
+    ys = []
+    for flags in (rans.F_WORDS_ALWAYS, rans.F_WORDS_REFILL):
+        m = rans.RansMatrix(enc, torch.from_numpy(step), lib, flags=flags)
+        np.testing.assert_array_equal(m.decode_codes().cpu().numpy(), codes)
+        y4 = m.gemv(x).cpu()
+        y3 = m.gemv(x[:3].contiguous()).cpu()
+        y1 = m.gemv(x[1]).cpu()
+        for b in range(4):
+            assert _rel_l2(y4[b].numpy(), ref[b]) <= REL_L2
+        assert _rel_l2(y3.numpy(), ref[:3]) <= REL_L2
+        assert _rel_l2(y1.numpy(), ref[1]) <= REL_L2
+        ys.append((y4, y3, y1))
+    for a, b in zip(*ys):
+        assert torch.equal(a, b)

@@ -68,27 +68,47 @@ def test_escapes_round_trip(rans, oracle):
     codes[0, 0] = -128  # the reference alphabet's lowest code is an escape here
     codes[5, 7] = 2 ** 30
     codes[6, 8] = -(2 ** 31)
-    enc = rans.encode(codes, 4, 128, 1)
-    assert len(enc["esc_col"]) == int(((codes < -127) | (codes > 127)).sum())
+    R, C = 4, 128
+    enc = rans.encode(codes, R, C, 1)
+    esc = (codes < -127) | (codes > 127)
+    assert len(enc["esc_pos"]) == int(esc.sum())
     np.testing.assert_array_equal(rans.decode_ref(enc), codes)
     np.testing.assert_array_equal(oracle.w64_decode(enc), codes)
-    # side table is CSR by row with ascending columns
-    rp = enc["esc_rowptr"]
-    for r in range(codes.shape[0]):
-        cols = enc["esc_col"][rp[r]:rp[r + 1]]
-        assert np.all(np.diff(cols) > 0)
+    # side table per tile, in column order (rows ascending within a column),
+    # rebuilt here by brute force from the codes
+    ncb = codes.shape[1] // C
+    tp = enc["esc_tileptr"]
+    assert tp[0] == 0 and tp[-1] == len(enc["esc_pos"]) and len(tp) == codes.size // (R * C) + 1
+    for t in range(len(tp) - 1):
+        rb, cb = divmod(t, ncb)
+        want_pos, want_val = [], []
+        for c in range(C):
+            for r in range(R):
+                v = codes[rb * R + r, cb * C + c]
+                if esc[rb * R + r, cb * C + c]:
+                    want_pos.append(c * 256 + r)
+                    want_val.append(v)
+        np.testing.assert_array_equal(enc["esc_pos"][tp[t]:tp[t + 1]], want_pos)
+        np.testing.assert_array_equal(enc["esc_val"][tp[t]:tp[t + 1]], want_val)
 
 
 def test_escape_side_table_must_match_stream(rans, oracle):
     codes = oracle.synth_codes(64, 256, 3.0, seed=3)
     codes[3, 4] = 500
     enc = rans.encode(codes, 4, 256, 1)
-    bad = dict(enc)
-    bad["esc_col"] = enc["esc_col"] + 1
-    with pytest.raises(AssertionError):
-        rans.decode_ref(bad)
-    with pytest.raises(AssertionError):
-        oracle.w64_decode(bad)
+    codes[2, 9] = -300
+    enc = rans.encode(codes, 4, 256, 1)
+    np.testing.assert_array_equal(enc["esc_pos"], [4 * 256 + 3, 9 * 256 + 2])
+    pos, val = enc["esc_pos"], enc["esc_val"]
+    for bad_pos, bad_val in [(pos + 256, val),                 # one column to the right
+                             (pos[::-1].copy(), val[::-1].copy()),  # not ascending
+                             (pos + 4, val),                   # tile rows 7 and 6 of 4
+                             (np.array([pos[0], pos[0]], np.int32), val)]:  # one entry twice
+        bad = dict(enc, esc_pos=bad_pos.astype(np.int32), esc_val=bad_val.astype(np.int32))
+        with pytest.raises(AssertionError):
+            rans.decode_ref(bad)
+        with pytest.raises(AssertionError):
+            oracle.w64_decode(bad)
 
 
 def test_corrupt_state_detected(rans, oracle):

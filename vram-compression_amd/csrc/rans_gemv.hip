@@ -73,8 +73,8 @@ struct GemvArgs {
     const uint16_t* soffs;
     const uint32_t* states;
     const uint4* table_lds;  // 2048 x 16 B LDS image of the table
-    const int32_t* esc_rowptr;
-    const int32_t* esc_col;
+    const int32_t* esc_tileptr;
+    const int32_t* esc_pos;
     const int32_t* esc_val;
     const float* step;
     const void* x;
@@ -93,8 +93,8 @@ struct DecodeArgs {
     const uint16_t* soffs;
     const uint32_t* states;
     const uint4* table_lds;
-    const int32_t* esc_rowptr;
-    const int32_t* esc_col;
+    const int32_t* esc_tileptr;
+    const int32_t* esc_pos;
     const int32_t* esc_val;
     const float* step;
     void* out;
@@ -307,16 +307,12 @@ __device__ __forceinline__ int32_t rans_step(uint32_t& st, uint32_t& a, uint32_t
     return entry_code(cur);
 }
 
-// Adds escape entry e (of this tile row's CSR range, rp holding the row
-// pointers of rows rb*R .. rb*R+R in lanes 0..R) to the lane's accumulator
-// of its row; v[b] is value*step*x[b] (0 for a lane without an entry).
+// Adds an escape entry at tile row re to the lane's accumulators; v[b] is
+// value*step*x[b] (0 for a lane without an entry).  A 0/1 weight per row and
+// one FMA per (row, batch): 2R + RB instructions rather than R + 2RB for a
+// select and an add.
 template <int R, int B>
-__device__ __forceinline__ void add_escape(float (&acc)[R][B], int rp, int e, const float (&v)[B]) {
-    int re = 0;
-#pragma unroll
-    for (int r = 1; r < R; r++) re += e >= __builtin_amdgcn_readlane(rp, r) ? 1 : 0;
-    // a 0/1 weight per row and one FMA per (row, batch): 2R + RB
-    // instructions rather than R + 2RB for a select and an add
+__device__ __forceinline__ void add_escape(float (&acc)[R][B], int re, const float (&v)[B]) {
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const float m = re == r ? 1.f : 0.f;
@@ -344,7 +340,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     // Every kernel argument the prologue needs, fetched in one scalar batch
     // (otherwise each is loaded, and waited for, at its first use).
     asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.soffs), "s"(a.table_lds),
-                 "s"(a.words), "s"(a.x), "s"(a.step), "s"(a.esc_rowptr), "s"(a.esc_col),
+                 "s"(a.words), "s"(a.x), "s"(a.step), "s"(a.esc_tileptr), "s"(a.esc_pos),
                  "s"(a.esc_val), "s"(a.C), "s"(a.cols),
                  "s"(a.L.raw_words), "s"(a.W), "s"(a.ncb), "s"(a.ngroups));
 
@@ -356,8 +352,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     // The tile extent is loaded first: the block copy waits for it, and
     // loads complete in order, so nothing issued after it delays that copy.
     const TileOff to = load_tile_off(a.tile_off, t);
-    // Row pointers of this tile row's escapes (lanes 0..R), also needed early.
-    const int rp = a.esc_rowptr[rb * R + min(lane, R)];
+    // This tile's range of the escape side table (lanes 0, 1), also needed early.
+    const int tp = a.esc_tileptr[t + min(lane, 1)];
     asm volatile("" ::: "memory");  // keep these two loads first
     uint32_t st0[S], off0[S];
 #pragma unroll
@@ -405,27 +401,32 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     load_block(0);
     uint32_t o0, n16;
     tile_extent(to, true, a.L.raw_words, o0, n16);
-    // Escapes of this tile row are added by column group 0, in chunks of 64
-    // side-table entries: chunk k goes to wave k mod W.  The row pointers
-    // are read here, before the copies, while the wait for them is exact;
-    // the wave's first chunk is requested behind the copies (so waiting for
-    // it costs nothing more), and its x and step gathers go out before the
+    // Each wave adds its own tile's escapes, in chunks of 64 side-table
+    // entries.  They run in column order within the tile, so a chunk's x and
+    // step gathers fall in a narrow column range (a few cache lines).  The
+    // range is read here, before the copies, while the wait for it is exact;
+    // the first chunks are requested behind the copies (so waiting for them
+    // costs nothing more), and their x and step gathers go out before the
     // decode loop, their values kept raw until after the loop, so that
     // latency overlaps the decode.
-    const bool esc = a.has_esc && g == 0;  // kernel-uniform
-    const int e_lo = esc ? __builtin_amdgcn_readlane(rp, 0) : 0;
-    const int e_hi = esc ? __builtin_amdgcn_readlane(rp, R) : 0;
+    const bool esc = a.has_esc;  // kernel-uniform
+    const int e_lo = esc ? __builtin_amdgcn_readlane(tp, 0) : 0;
+    const int e_hi = esc ? __builtin_amdgcn_readlane(tp, 1) : 0;
     asm volatile("" ::"s"(e_lo), "s"(e_hi));
     stage_tile(raw, a.words, o0, n16, lane);
     stage_table(tab, a.table_lds, wave, W, lane);
-    constexpr int P = 2;  // chunks per wave prefetched: up to 64*P*W escapes per tile row
-    int ecol[P], eval[P];
+    constexpr int P = 2;  // chunks per wave prefetched: 128 escapes per tile
+    const int cbase = cb * a.C;
+    // tile column of an entry, clamped into the tile so that no side-table
+    // content can send a gather outside x or step
+    auto esc_col = [&](int pos) { return cbase + (int)min((uint32_t)pos >> 8, (uint32_t)(a.C - 1)); };
+    int epos[P], eval[P];
 #pragma unroll
     for (int p = 0; p < P; p++) {
-        ecol[p] = eval[p] = 0;
-        if (e_lo + 64 * (wave + p * W) < e_hi) {  // wave-uniform
-            const int ec = min(e_lo + 64 * (wave + p * W) + lane, e_hi - 1);
-            ecol[p] = a.esc_col[ec];
+        epos[p] = eval[p] = 0;
+        if (e_lo + 64 * p < e_hi) {  // wave-uniform
+            const int ec = min(e_lo + 64 * p + lane, e_hi - 1);
+            epos[p] = a.esc_pos[ec];
             eval[p] = a.esc_val[ec];
         }
     }
@@ -459,17 +460,19 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     };
     // Escape gathers: issued in the first iteration behind the prefetch of
     // the second block, so the first wait that can drain them comes a block
-    // of decode later.  Unconditional (column 0 for a wave without a chunk):
-    // no branch, so no register merges that would wait for them early.
+    // of decode later.  Unconditional (the tile's first column for a wave
+    // without a chunk): no branch, so no register merges that would wait
+    // for them early.
     uint32_t exr[P][B], esr[P];
     auto gather = [&]() {
 #pragma unroll
         for (int p = 0; p < P; p++) {
-            asm volatile("" : "+v"(ecol[p]), "+v"(eval[p]));
-            esr[p] = __float_as_uint(a.step[ecol[p]]);
+            asm volatile("" : "+v"(epos[p]), "+v"(eval[p]));
+            const int col = esc_col(epos[p]);
+            esr[p] = __float_as_uint(a.step[col]);
 #pragma unroll
             for (int b = 0; b < B; b++)
-                exr[p][b] = load_x_bits(a.x, (int64_t)b * a.cols + ecol[p], XBF16);
+                exr[p][b] = load_x_bits(a.x, (int64_t)b * a.cols + col, XBF16);
         }
     };
 
@@ -513,26 +516,27 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     float ev[B];
 #pragma unroll
     for (int p = 0; p < P; p++) {
-        const int e = e_lo + 64 * (wave + p * W) + lane;
-        if (e_lo + 64 * (wave + p * W) < e_hi) {
+        const int e = e_lo + 64 * p + lane;
+        if (e_lo + 64 * p < e_hi) {
             asm volatile("" : "+v"(esr[p]));
 #pragma unroll
             for (int b = 0; b < B; b++) asm volatile("" : "+v"(exr[p][b]));
             const float ve = e < e_hi ? (float)eval[p] * __uint_as_float(esr[p]) : 0.f;
 #pragma unroll
             for (int b = 0; b < B; b++) ev[b] = ve * bits_to_x(exr[p][b], XBF16);
-            add_escape<R, B>(acc, rp, e, ev);
+            add_escape<R, B>(acc, epos[p] & 0xFF, ev);
         }
     }
-    // further chunks (tile rows with more than 64*P*W escapes)
-    for (int e0 = e_lo + 64 * (wave + P * W); e0 < e_hi; e0 += 64 * W) {
+    // further chunks (tiles with more than 64*P escapes)
+    for (int e0 = e_lo + 64 * P; e0 < e_hi; e0 += 64) {
         const int e = e0 + lane;
         const int ec = min(e, e_hi - 1);
-        const int col = a.esc_col[ec];
+        const int pos = a.esc_pos[ec];
+        const int col = esc_col(pos);
         const float ve = e < e_hi ? (float)a.esc_val[ec] * a.step[col] : 0.f;
 #pragma unroll
         for (int b = 0; b < B; b++) ev[b] = ve * load_x(a.x, (int64_t)b * a.cols + col, XBF16);
-        add_escape<R, B>(acc, rp, e, ev);
+        add_escape<R, B>(acc, pos & 0xFF, ev);
     }
 
     constexpr int NRB = R * B;
@@ -628,11 +632,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
     const int tc = active ? t : a.ntiles - 1;
     const int rb = tc / a.ncb, cb = tc - rb * a.ncb;
     asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.soffs), "s"(a.table_lds),
-                 "s"(a.words), "s"(a.step), "s"(a.esc_rowptr), "s"(a.out), "s"(a.C),
+                 "s"(a.words), "s"(a.step), "s"(a.esc_tileptr), "s"(a.out), "s"(a.C),
                  "s"(a.cols), "s"(a.L.raw_words), "s"(a.W), "s"(a.ncb), "s"(a.ntiles));
 
     const TileOff to = load_tile_off(a.tile_off, tc);
-    const int rp = a.esc_rowptr[rb * R + min(lane, R)];
+    const int tp = a.esc_tileptr[tc + min(lane, 1)];
     asm volatile("" ::: "memory");  // keep these two loads first
     uint32_t st0[S], off0[S];
 #pragma unroll
@@ -702,24 +706,24 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
         }
     }
 
-    // Escapes of this tile: side-table entries of its rows whose column lies
-    // in [cb*C, cb*C + C).  The wave's own stores complete first, so the
-    // value lands after the 0 its position was decoded as.
+    // Escapes of this tile: its own side-table entries, written over the 0
+    // each escape position was decoded as.  The wave's own stores complete
+    // first, so the value lands after that 0.  Positions are clamped into
+    // the tile, so no side-table content can address outside the output.
     if (!a.has_esc) return;
     wait_vm();
-    const int cmin = cb * a.C, cmax = cmin + a.C;
-    for (int r = 0; r < R; r++) {
-        const int e0 = __builtin_amdgcn_readlane(rp, r), e1 = __builtin_amdgcn_readlane(rp, r + 1);
-        for (int e = e0 + lane; e < e1; e += 64) {
-            const int col = a.esc_col[e];
-            if (col < cmin || col >= cmax) continue;
-            const int32_t v = a.esc_val[e];
-            if (MODE == 0)
-                __builtin_amdgcn_raw_buffer_store_b32(v, ors, col * 4, r * a.cols * 4, 0);
-            else
-                __builtin_amdgcn_raw_buffer_store_b16(to_bf16((float)v * a.step[col]), ors, col * 2,
-                                                      r * a.cols * 2, 0);
-        }
+    const int e_lo = __builtin_amdgcn_readlane(tp, 0), e_hi = __builtin_amdgcn_readlane(tp, 1);
+    const int cbase = cb * a.C;
+    for (int e = e_lo + lane; e < e_hi; e += 64) {
+        const int pos = a.esc_pos[e];
+        const int r = min(pos & 0xFF, R - 1);
+        const int col = cbase + (int)min((uint32_t)pos >> 8, (uint32_t)(a.C - 1));
+        const int32_t v = a.esc_val[e];
+        if (MODE == 0)
+            __builtin_amdgcn_raw_buffer_store_b32(v, ors, (r * a.cols + col) * 4, 0, 0);
+        else
+            __builtin_amdgcn_raw_buffer_store_b16(to_bf16((float)v * a.step[col]), ors,
+                                                  (r * a.cols + col) * 2, 0, 0);
     }
 }
 
@@ -781,7 +785,7 @@ bool valid_geometry(const rans_w64_matrix* m) {
 
 bool valid_pointers(const rans_w64_matrix* m) {
     return m->words && m->tile_off && m->soffs && m->states && m->table_lds && m->step &&
-           m->esc_rowptr && m->esc_col && m->esc_val;
+           m->esc_tileptr && m->esc_pos && m->esc_val;
 }
 
 // Waves per GEMV workgroup: the largest divisor of ncb up to kMaxWaves whose
@@ -914,8 +918,8 @@ int launch_decode_common(const rans_w64_matrix* m, void* out, hipStream_t stream
     a.soffs = m->soffs;
     a.states = m->states;
     a.table_lds = reinterpret_cast<const uint4*>(m->table_lds);
-    a.esc_rowptr = m->esc_rowptr;
-    a.esc_col = m->esc_col;
+    a.esc_tileptr = m->esc_tileptr;
+    a.esc_pos = m->esc_pos;
     a.esc_val = m->esc_val;
     a.step = m->step;
     a.out = out;
@@ -958,7 +962,7 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
     const bool xbf16 = x_dtype == RANS_X_BF16;
     const size_t xsz = xbf16 ? 2 : 4;
     const int fetch = m->flags & RANS_F_WORDS_MASK;
-    const bool refill = fetch == RANS_F_WORDS_REFILL || (fetch == 0 && m->R >= 8);
+    const bool refill = fetch == RANS_F_WORDS_REFILL || (fetch == 0 && m->R >= 3);
     const int var = (xbf16 ? 1 : 0) | (refill ? 2 : 0);
 
     GemvArgs a;
@@ -967,8 +971,8 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
     a.soffs = m->soffs;
     a.states = m->states;
     a.table_lds = reinterpret_cast<const uint4*>(m->table_lds);
-    a.esc_rowptr = m->esc_rowptr;
-    a.esc_col = m->esc_col;
+    a.esc_tileptr = m->esc_tileptr;
+    a.esc_pos = m->esc_pos;
     a.esc_val = m->esc_val;
     a.step = m->step;
     a.rows = m->rows;

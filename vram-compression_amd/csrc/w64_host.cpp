@@ -27,7 +27,7 @@ struct Encoded {
     std::vector<uint32_t> states;
     uint32_t table[kM];
     int64_t freq[256];
-    std::vector<int32_t> esc_rowptr, esc_col, esc_val;
+    std::vector<int32_t> esc_tileptr, esc_pos, esc_val;
     int64_t payload_words = 0;
     int32_t max_tile_words = 0;
     int32_t max_state_words = 0;  // longest state stream, counting the tile padding
@@ -110,26 +110,15 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
     if (!codes || !handle || !info || rows <= 0 || cols <= 0 || R <= 0 || C <= 0 || S <= 0)
         return RANS_EARG;
     if (rows % R || cols % C || C % (64 * S)) return RANS_EGEOMETRY;
+    if (R > 256 || C >= (1 << 23)) return RANS_EGEOMETRY;  // esc_pos packing
     const int64_t N = (int64_t)rows * cols;
     auto* E = new Encoded();
 
-    // Symbols and the escape side table.
+    // Symbols; the escape side table is collected per tile below.
     std::vector<uint8_t> sym((size_t)N);
-    E->esc_rowptr.assign((size_t)rows + 1, 0);
-    for (int32_t r = 0; r < rows; r++) {
-        const int32_t* row = codes + (int64_t)r * cols;
-        uint8_t* srow = sym.data() + (int64_t)r * cols;
-        for (int32_t c = 0; c < cols; c++) {
-            const int32_t v = row[c];
-            if (v >= -127 && v <= 127) {
-                srow[c] = (uint8_t)(v + 128);
-            } else {
-                srow[c] = kEsc;
-                E->esc_col.push_back(c);
-                E->esc_val.push_back(v);
-            }
-        }
-        E->esc_rowptr[(size_t)r + 1] = (int32_t)E->esc_col.size();
+    for (int64_t i = 0; i < N; i++) {
+        const int32_t v = codes[i];
+        sym[(size_t)i] = v >= -127 && v <= 127 ? (uint8_t)(v + 128) : (uint8_t)kEsc;
     }
 
     int64_t cum[256];
@@ -150,6 +139,7 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
     std::vector<int64_t> payload((size_t)ntiles, 0);
     std::vector<int> too_big((size_t)ntiles, 0);
     std::vector<int32_t> longest((size_t)ntiles, 0);
+    std::vector<std::vector<int32_t>> tesc_pos((size_t)ntiles), tesc_val((size_t)ntiles);
 
     const int64_t* freq = E->freq;
     parallel_for(ntiles, nthreads > 0 ? nthreads : 1, [&](int64_t t) {
@@ -200,6 +190,15 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
             lmax = std::max<int32_t>(lmax, (int32_t)(end - E->soffs[sid]));
         }
         longest[(size_t)t] = lmax;
+        // the tile's escapes in column order, rows ascending within a column
+        for (int32_t c = 0; c < C; c++)
+            for (int32_t r = 0; r < R; r++) {
+                const int64_t i = ((int64_t)rb * R + r) * cols + (int64_t)cb * C + c;
+                if (sym[(size_t)i] == kEsc) {
+                    tesc_pos[(size_t)t].push_back((c << 8) | r);
+                    tesc_val[(size_t)t].push_back(codes[i]);
+                }
+            }
     });
     for (int64_t t = 0; t < ntiles; t++) {
         if (too_big[(size_t)t]) {
@@ -222,6 +221,23 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
         return RANS_ETILE;
     }
     E->tile_off[(size_t)ntiles] = (uint32_t)total;
+    E->esc_tileptr.assign((size_t)ntiles + 1, 0);
+    int64_t nesc = 0;
+    for (int64_t t = 0; t < ntiles; t++) {
+        E->esc_tileptr[(size_t)t] = (int32_t)nesc;
+        nesc += (int64_t)tesc_pos[(size_t)t].size();
+    }
+    if (nesc > 0x7FFFFFFFll) {
+        delete E;
+        return RANS_ETILE;
+    }
+    E->esc_tileptr[(size_t)ntiles] = (int32_t)nesc;
+    E->esc_pos.reserve((size_t)nesc);
+    E->esc_val.reserve((size_t)nesc);
+    for (int64_t t = 0; t < ntiles; t++) {
+        E->esc_pos.insert(E->esc_pos.end(), tesc_pos[(size_t)t].begin(), tesc_pos[(size_t)t].end());
+        E->esc_val.insert(E->esc_val.end(), tesc_val[(size_t)t].begin(), tesc_val[(size_t)t].end());
+    }
     E->words.resize((size_t)total);
     parallel_for(ntiles, nthreads > 0 ? nthreads : 1, [&](int64_t t) {
         std::memcpy(E->words.data() + E->tile_off[(size_t)t], blocks[(size_t)t].data(),
@@ -231,7 +247,7 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
     info[0] = total;
     info[1] = ntiles;
     info[2] = ntiles * nst;
-    info[3] = (int64_t)E->esc_col.size();
+    info[3] = (int64_t)E->esc_pos.size();
     info[4] = E->max_tile_words;
     info[5] = E->payload_words;
     info[6] = E->max_state_words;
@@ -241,7 +257,7 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
 
 extern "C" int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off,
                                      uint16_t* soffs, uint32_t* states, uint32_t* table,
-                                     int64_t* freq, int32_t* esc_rowptr, int32_t* esc_col,
+                                     int64_t* freq, int32_t* esc_tileptr, int32_t* esc_pos,
                                      int32_t* esc_val) {
     if (!handle) return RANS_EARG;
     auto* E = static_cast<Encoded*>(handle);
@@ -252,8 +268,8 @@ extern "C" int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* ti
     put(tile_off, E->tile_off);
     put(soffs, E->soffs);
     put(states, E->states);
-    put(esc_rowptr, E->esc_rowptr);
-    put(esc_col, E->esc_col);
+    put(esc_tileptr, E->esc_tileptr);
+    put(esc_pos, E->esc_pos);
     put(esc_val, E->esc_val);
     if (table) std::memcpy(table, E->table, sizeof(E->table));
     if (freq) std::memcpy(freq, E->freq, sizeof(E->freq));
@@ -293,15 +309,24 @@ extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
         }
     }
     // The escape symbol decodes to kEsc-128; the side table must name exactly
-    // those positions.
+    // those positions: the same count, each entry inside its tile on an
+    // escape symbol, strictly ascending within the tile (so none twice).
     int64_t nesc_stream = 0;
     for (int64_t i = 0; i < (int64_t)rows * cols; i++) nesc_stream += out[i] == kEsc - 128;
-    const int64_t nesc = m->esc_rowptr ? m->esc_rowptr[rows] : 0;
+    const int64_t nesc = m->esc_tileptr ? m->esc_tileptr[ntiles] : 0;
     if (nesc != nesc_stream) return RANS_EARG;
-    for (int32_t r = 0; r < rows && nesc; r++) {
-        for (int32_t e = m->esc_rowptr[r]; e < m->esc_rowptr[r + 1]; e++) {
-            if (m->esc_col[e] < 0 || m->esc_col[e] >= cols) return RANS_EARG;
-            int32_t* o = out + (int64_t)r * cols + m->esc_col[e];
+    if (!nesc) return 0;
+    if (!m->esc_pos || !m->esc_val || m->esc_tileptr[0] != 0) return RANS_EARG;
+    for (int64_t t = 0; t < ntiles; t++) {
+        const int32_t rb = (int32_t)(t / ncb), cb = (int32_t)(t % ncb);
+        const int32_t lo = m->esc_tileptr[t], hi = m->esc_tileptr[t + 1];
+        if (lo > hi || hi > nesc) return RANS_EARG;
+        for (int32_t e = lo; e < hi; e++) {
+            const int32_t pos = m->esc_pos[e];
+            const int32_t r = pos & 0xFF, c = pos >> 8;
+            if (pos < 0 || r >= R || c >= C || (e > lo && pos <= m->esc_pos[e - 1]))
+                return RANS_EARG;
+            int32_t* o = out + ((int64_t)rb * R + r) * cols + (int64_t)cb * C + c;
             if (*o != kEsc - 128) return RANS_EARG;
             *o = m->esc_val[e];
         }

@@ -53,8 +53,8 @@ class RansMatrixDesc(ctypes.Structure):
                 ("words", ctypes.c_void_p), ("tile_off", ctypes.c_void_p),
                 ("soffs", ctypes.c_void_p), ("states", ctypes.c_void_p),
                 ("table", ctypes.c_void_p), ("table_lds", ctypes.c_void_p),
-                ("esc_rowptr", ctypes.c_void_p),
-                ("esc_col", ctypes.c_void_p), ("esc_val", ctypes.c_void_p),
+                ("esc_tileptr", ctypes.c_void_p),
+                ("esc_pos", ctypes.c_void_p), ("esc_val", ctypes.c_void_p),
                 ("step", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
                 ("workspace_bytes", ctypes.c_int64)]
 
@@ -185,6 +185,7 @@ def encode(codes, R, C, S=1, threads=None):
     rc = lib.rans_w64_encode(_p(codes), rows, cols, R, C, S, nthreads, ctypes.byref(h), _p(info))
     assert rc != -5, "degenerate distribution (single symbol)"
     assert rc != -6, "a tile needs more than 65535 words: use smaller R or C"
+    assert rc != -2, "tile geometry outside the format (R <= 256, C < 2^23)"
     assert rc == 0, f"encode failed ({rc})"
     nwords, ntiles, nstates, nesc, max_tile_words, payload_words, max_state_words = \
         (int(v) for v in info)
@@ -194,12 +195,12 @@ def encode(codes, R, C, S=1, threads=None):
     states = np.zeros(nstates, np.uint32)
     table = np.zeros(M, np.uint32)
     freq = np.zeros(256, np.int64)
-    esc_rowptr = np.zeros(rows + 1, np.int32)
-    esc_col = np.zeros(nesc, np.int32)
+    esc_tileptr = np.zeros(ntiles + 1, np.int32)
+    esc_pos = np.zeros(nesc, np.int32)
     esc_val = np.zeros(nesc, np.int32)
     try:
         rc = lib.rans_w64_encode_fetch(h, _p(words), _p(tile_off), _p(soffs), _p(states),
-                                       _p(table), _p(freq), _p(esc_rowptr), _p(esc_col),
+                                       _p(table), _p(freq), _p(esc_tileptr), _p(esc_pos),
                                        _p(esc_val))
         assert rc == 0
     finally:
@@ -209,13 +210,13 @@ def encode(codes, R, C, S=1, threads=None):
     p = freq[sym.ravel()] / M
     pad_words = nwords - payload_words
     return dict(words=words, tile_off=tile_off, soffs=soffs, states=states, table=table,
-                esc_rowptr=esc_rowptr, esc_col=esc_col, esc_val=esc_val,
+                esc_tileptr=esc_tileptr, esc_pos=esc_pos, esc_val=esc_val,
                 R=R, C=C, S=S, shape=codes.shape, max_tile_words=max_tile_words,
                 max_state_words=max_state_words,
                 bits_payload=16 * payload_words / N,
                 bits_state_offs=(48 * nstates + 32 * (ntiles + 1) + 16 * pad_words) / N,
                 bits_table=32 * M / N,
-                bits_escape=32 * (rows + 1 + 2 * nesc) / N,
+                bits_escape=32 * (ntiles + 1 + 2 * nesc) / N,
                 entropy_model=float(-np.log2(p).mean()))
 
 
@@ -226,9 +227,13 @@ def pick_tiling(rows, cols, R=None, S=1, target_states=None):
     - states: about 105 symbols per state for mid-size matrices (at
       1536x8960 that is 2048 waves, two per SIMD: two waves on a SIMD slow
       each other by only ~15%, so a one-wave SIMD is mostly idle capacity);
-      small ones get more states, down to 64 symbols each; matrices above
-      32M weights use about 160 symbols per state.  Fewer states cost less
-      per-state overhead (48 bits each), more states give more parallelism.
+      small ones get more states: up to 98304 at 64 or more symbols each,
+      and at least 49152 (768 waves) down to 35 symbols each, below which
+      the launch is latency-bound far above its byte count (1536x1536 at
+      3.25 bits: 5.5 us with 49152 states, 8.1 us with 36864, +0.21
+      bits/weight); matrices above 32M weights use about 160 symbols per
+      state.  Fewer states cost less per-state overhead (48 bits each),
+      more states give more parallelism.
     - column tiles per tile row (ncb): 8 is best (8 waves of a workgroup
       share one LDS table, so more waves fit per CU), then 4-7 and 16 (the
       latter needs the split-K reduction); fewer than 4 repeat the table
@@ -243,7 +248,7 @@ def pick_tiling(rows, cols, R=None, S=1, target_states=None):
     elif n >= (32 << 20):
         target = n // 160
     else:
-        target = int(min(max(n // 105, min(98304, n // 64)), 262144))
+        target = int(min(max(n // 105, min(98304, n // 64), min(49152, n // 35)), 262144))
     best = None
     for r in Rs:
         for c in cands:
@@ -266,7 +271,7 @@ def pick_tiling(rows, cols, R=None, S=1, target_states=None):
 def _host_desc(enc, keep):
     """rans_w64_matrix over host numpy arrays (for rans_w64_decode_host)."""
     arrs = {k: np.ascontiguousarray(enc[k]) for k in
-            ("words", "tile_off", "soffs", "states", "table", "esc_rowptr", "esc_col", "esc_val")}
+            ("words", "tile_off", "soffs", "states", "table", "esc_tileptr", "esc_pos", "esc_val")}
     keep.append(arrs)
     rows, cols = enc["shape"]
     d = RansMatrixDesc(rows=rows, cols=cols, R=enc["R"], C=enc["C"], S=enc["S"],
@@ -325,9 +330,9 @@ class RansMatrix:
         # the kernels read the table's LDS image; the packed table is only
         # for the host decoder and stays on the host
         self.table_lds = up(table_lds(enc["table"], lib), np.int32)
-        self.esc_rowptr = up(enc["esc_rowptr"], np.int32)
+        self.esc_tileptr = up(enc["esc_tileptr"], np.int32)
         # never hand a zero-length buffer's (possibly null) pointer to the ABI
-        self.esc_col = up(enc["esc_col"] if len(enc["esc_col"]) else np.zeros(1, np.int32), np.int32)
+        self.esc_pos = up(enc["esc_pos"] if len(enc["esc_pos"]) else np.zeros(1, np.int32), np.int32)
         self.esc_val = up(enc["esc_val"] if len(enc["esc_val"]) else np.zeros(1, np.int32), np.int32)
         step = torch.as_tensor(step)
         assert step.numel() == self.cols, "step must have one value per column"
@@ -337,19 +342,19 @@ class RansMatrix:
         self._desc = RansMatrixDesc(
             rows=self.rows, cols=self.cols, R=self.R, C=self.C, S=self.S,
             max_tile_words=self.max_tile_words, max_state_words=self.max_state_words,
-            flags=(int(flags) & F_WORDS_MASK) | (0 if len(enc["esc_col"]) else F_NO_ESCAPES),
+            flags=(int(flags) & F_WORDS_MASK) | (0 if len(enc["esc_pos"]) else F_NO_ESCAPES),
             words=self.words.data_ptr(), tile_off=self.tile_off.data_ptr(),
             soffs=self.soffs.data_ptr(), states=self.states.data_ptr(),
             table=None, table_lds=self.table_lds.data_ptr(),
-            esc_rowptr=self.esc_rowptr.data_ptr(),
-            esc_col=self.esc_col.data_ptr(), esc_val=self.esc_val.data_ptr(),
+            esc_tileptr=self.esc_tileptr.data_ptr(),
+            esc_pos=self.esc_pos.data_ptr(), esc_val=self.esc_val.data_ptr(),
             step=self.step.data_ptr(), workspace=None, workspace_bytes=0)
         self.workspace = None
         self._ensure_workspace(4)
         # device bytes (the 32 KB table image in place of the 16 KB table)
         self.nbytes = sum(t.numel() * t.element_size() for t in
                           (self.words, self.tile_off, self.soffs, self.states, self.table_lds,
-                           self.esc_rowptr)) + 8 * int(len(enc["esc_col"]))
+                           self.esc_tileptr)) + 8 * int(len(enc["esc_pos"]))
 
     def tune(self, batch=1, x_dtype=torch.bfloat16, iters=20):
         """Time the two word-fetch policies of the GEMV on this matrix and

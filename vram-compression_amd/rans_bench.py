@@ -254,12 +254,10 @@ def qwen15b_layer_shapes():
 
 
 def chain_tiling(rows, cols):
-    """Tiling for one matrix of the per-token chain: about 105 symbols per
-    state on large matrices, fewer on small ones (whose decode would
-    otherwise be latency-bound far above their byte count)."""
-    n = rows * cols
-    target = max(n // 105, min(n // 35, 49152))
-    return pick_tiling(rows, cols, S=1, target_states=target)
+    """Tiling for one matrix of the per-token chain: the library's default
+    (about 105 symbols per state on large matrices, at least 768 waves on
+    small ones)."""
+    return pick_tiling(rows, cols, S=1)
 
 
 def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None, C=None, S=1,
@@ -288,7 +286,7 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
     out = dict(rows=rows, cols=cols, bits_target=bits, dist=dist, escape_frac=escape_frac,
                batch=batch, R=R, C=C, S=S, word_fetch={1: "always", 2: "refill"}[flags & 3],
                entropy=entropy_fast(codes),
-               bits_total=8 * m.nbytes / codes.size, n_escapes=int(len(enc["esc_col"])),
+               bits_total=8 * m.nbytes / codes.size, n_escapes=int(len(enc["esc_pos"])),
                t_rans_us=t_rans, t_bf16_us=t_bf16,
                effective_GBps=rows * cols * 2 / t_rans / 1e3,
                compressed_GBps=m.nbytes / t_rans / 1e3,
