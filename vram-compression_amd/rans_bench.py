@@ -379,5 +379,29 @@ def configs():
           flush=True)
 
 
+def profile(rows=25600, cols=5120, bits=2.25, dist="student3", escape_frac=0.01, R=16, C=640,
+            launches=20, fetch="refill"):
+    """One encoded matrix launched `launches` times at batch 1, then at
+    batch 4 (bf16 x), for a profiler run: rans_bench.py profile [ROWS COLS
+    BITS DIST ESC R C LAUNCHES FETCH].  The defaults are the 27B-class
+    25600x5120 matrix of the configurations."""
+    lib = rans.build()
+    codes = synth_codes_full(rows, cols, bits, dist=dist, seed=rows + cols, escape_frac=escape_frac)
+    step = torch.from_numpy(lognormal_steps(cols, seed=rows + cols))
+    flags = {"always": rans.F_WORDS_ALWAYS, "refill": rans.F_WORDS_REFILL}[fetch]
+    m = rans.RansMatrix(encode(codes, R, C, 1), step, lib, flags=flags)
+    for batch in (1, 4):
+        x = torch.randn(batch, cols, device="cuda").bfloat16()
+        y = torch.empty(batch, rows, device="cuda")
+        for _ in range(launches):
+            m.gemv(x, y)
+        torch.cuda.synchronize()
+        print(f"profile {rows}x{cols} R={R} C={C} batch {batch}: {launches} launches", flush=True)
+
+
 if __name__ == "__main__":
-    {"test": test, "bench": bench, "configs": configs}[sys.argv[1]]()
+    if sys.argv[1] == "profile":
+        types = (int, int, float, str, float, int, int, int, str)
+        profile(*(t(v) for t, v in zip(types, sys.argv[2:])))
+    else:
+        {"test": test, "bench": bench, "configs": configs}[sys.argv[1]]()
