@@ -18,8 +18,8 @@
 //      loads x[c]*step[c] once (the waterfilling fold happens here, one block
 //      of column steps ahead of use) and reuses it for the R rows of the tile;
 //   5. row sums are reduced across the 64 lanes with cross-lane shuffles and
-//      across the W waves through LDS in a fixed order, escapes are added
-//      from the CSR side table, and y is written; when one workgroup does not
+//      across the W waves through LDS in a fixed order, each wave adds its
+//      tile's escapes from the side table, and y is written; when one workgroup does not
 //      cover all column tiles, partial sums go to a workspace and the last
 //      workgroup of the tile row adds them up in a fixed order (no atomics on
 //      y, no memset, deterministic).
@@ -672,7 +672,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
         __builtin_amdgcn_make_buffer_rsrc(obase, 0, R * a.cols * ESZ, kBufWord3);
     Lanes<S> L;
     init_lanes<S>(L, tab, raw, st0, off0);
-    for (int k0 = 0; k0 < nk; k0 += KU) {
+    // One block of nu <= KU column steps.  The loop below runs whole blocks
+    // only (nu = KU, no early exit): exits after 1, 2 or 3 steps' stores
+    // would meet at the loop latch, and the compiler would then wait there
+    // for the stores of the longest path.  A partial last block follows it.
+    auto run_block = [&](int k0, int nu) {
         float sv[KU][S];
         if (MODE == 1) {
 #pragma unroll
@@ -682,13 +686,18 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
                     asm volatile("" : "+v"(sr[u][s]));
                     sv[u][s] = sr[u][s];
                 }
-            if (k0 + KU < nk) load_steps(k0 + KU);
+            // unconditional: past the last block these read columns of the
+            // next tile, or 0 past the end of the matrix, and go unused.  A
+            // conditional prefetch merges two wait states at the join, and
+            // the compiler then waits for this block's stores as well
+            // (vmcnt counts stores too), once per block
+            load_steps(k0 + KU);
             asm volatile("" ::: "memory");
         }
         const int vb = (colbase + 64 * S * k0) * ESZ;
 #pragma unroll
         for (int u = 0; u < KU; u++) {
-            if (k0 + u >= nk) break;
+            if (u >= nu) break;
 #pragma unroll
             for (int r = 0; r < R; r++) {
 #pragma unroll
@@ -704,7 +713,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
                 }
             }
         }
-    }
+    };
+    const int nk_full = nk - nk % KU;
+    for (int k0 = 0; k0 < nk_full; k0 += KU) run_block(k0, KU);
+    if (nk_full < nk) run_block(nk_full, nk - nk_full);
 
     // Escapes of this tile: its own side-table entries, written over the 0
     // each escape position was decoded as.  The wave's own stores complete
