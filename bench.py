@@ -57,7 +57,7 @@ def algorithmic_bytes(enc, rows, cols, batch=1):
     holds it (payload and padding words, tile offsets, per-state offsets and
     initial states, the 32 KB LDS image of the table, the escape side table),
     x (bf16), the step vector (f32) and y (f32)."""
-    comp = (enc["words"].nbytes + enc["tile_off"].nbytes + enc["soffs"].nbytes +
+    comp = (enc["words"].nbytes + enc["tile_off"].nbytes + enc["slen"].nbytes +
             enc["states"].nbytes + 2 * enc["table"].nbytes + enc["esc_tileptr"].nbytes +
             enc["esc_pos"].nbytes + enc["esc_val"].nbytes)
     return comp, comp + cols * 2 * batch + cols * 4 + rows * 4 * batch

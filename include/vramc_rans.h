@@ -37,9 +37,13 @@
  *     entries run in column order (R <= 256).
  *   - words: all tile blocks concatenated; tile t's block is
  *     words[tile_off[t] .. tile_off[t+1]), a multiple of 8 words with at least
- *     one trailing pad word; state j's stream starts at tile_off[t]+soffs[t*64*S+j]
- *     and lists its renormalisation words in decode order.  states[] holds
- *     each state's initial (decoder) value.
+ *     one trailing pad word.  The streams of the tile's 64*S states follow
+ *     each other in state order, state j's holding slen[t*64*S+j] words (its
+ *     renormalisation words in decode order), so it starts at tile_off[t]
+ *     plus the lengths of states 0..j-1.  A stream of n symbols has at most
+ *     0.75n+1 words (12 bits per symbol at most), so lengths fit a byte for
+ *     up to 338 symbols per state (R*C/(64*S)).  states[] holds each
+ *     state's initial (decoder) value.
  */
 #ifndef VRAMC_RANS_H
 #define VRAMC_RANS_H
@@ -63,7 +67,7 @@ extern "C" {
 #define RANS_EWORKSPACE (-3)   /* split-K workspace missing or too small */
 #define RANS_EARG (-4)         /* null pointer or negative size */
 #define RANS_ECODES (-5)       /* encoder: degenerate or empty symbol distribution */
-#define RANS_ETILE (-6)        /* encoder: a tile block exceeds 65535 words */
+#define RANS_ETILE (-6)        /* encoder: a tile block exceeds 65535 words, or a state 255 */
 
 /* rans_w64_matrix.flags.  Word fetch (bits 0-1): how the GEMV fetches
  * renormalisation words; the decoded values are identical, only speed
@@ -83,7 +87,7 @@ typedef struct rans_w64_matrix {
     int32_t flags;            /* RANS_F_* launch options, 0 for the defaults */
     const uint16_t* words;    /* [tile_off[ntiles]] */
     const uint32_t* tile_off; /* [ntiles+1], in words, multiples of 8 */
-    const uint16_t* soffs;    /* [ntiles*64*S] */
+    const uint8_t* slen;      /* [ntiles*64*S], words in each state's stream */
     const uint32_t* states;   /* [ntiles*64*S] */
     const uint32_t* table;    /* [4096], reference packing (host decoder) */
     const uint32_t* table_lds;/* [8192], the table as the kernels hold it in LDS, made
@@ -144,15 +148,16 @@ int rans_table_lds(const uint32_t* table, uint32_t* out);
 
 /* Encode int32 codes (rows x cols, row-major) into the w64 format; replaces
  * encode() (rans.py:62-98).  R <= 256 and C < 2^23 (the side table's
- * position packing), else RANS_EGEOMETRY.  On success *handle owns the
- * result and info[]
+ * position packing), else RANS_EGEOMETRY; RANS_ETILE when a tile block
+ * exceeds 65535 words or a state's stream 255 words.  On success *handle
+ * owns the result and info[]
  * receives {nwords, ntiles, nstates, nesc, max_tile_words, payload_words,
  * max_state_words}.
  * Fetch the arrays with rans_w64_encode_fetch, then free the handle. */
 int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols, int32_t R, int32_t C,
                     int32_t S, int32_t nthreads, void** handle, int64_t* info);
 
-int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off, uint16_t* soffs,
+int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off, uint8_t* slen,
                           uint32_t* states, uint32_t* table, int64_t* freq,
                           int32_t* esc_tileptr, int32_t* esc_pos, int32_t* esc_val);
 

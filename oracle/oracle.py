@@ -268,7 +268,10 @@ def w64_decode(enc):
     ntiles = (rows // R) * (cols // C)
     nst = 64 * S
     n = (C // nst) * R
-    start = np.repeat(tile_off[:ntiles], nst) + enc["soffs"].astype(np.int64)
+    # streams follow each other in state order within a tile block
+    slen = enc["slen"].astype(np.int64).reshape(ntiles, nst)
+    starts_in_tile = np.cumsum(slen, axis=1) - slen
+    start = (tile_off[:ntiles, None] + starts_in_tile).ravel()
     out = np.zeros((ntiles * nst, n), np.uint8)
     w = np.ascontiguousarray(enc["words"], np.uint16)
     st0 = np.ascontiguousarray(enc["states"], np.uint32)

@@ -51,12 +51,15 @@ def test_streams_equal_reference_encoder(rans, oracle, shape):
     assert lib.orc_encode_lanes(p(seqs), lanes, n, p(freq), p(cum), p(words), cap, p(offs)) == 0
     assert lib.orc_count_words(p(seqs), lanes, n, p(freq), p(cum), p(counts)) == 0
     nst = 64 * S
+    # each state's stored length is its stream's word count, and the
+    # streams of a tile follow each other from the tile's offset
+    np.testing.assert_array_equal(enc["slen"], counts)
     for j in range(lanes):
         o = int(offs[j])
         assert int(enc["states"][j]) == (int(words[o]) << 16) | int(words[o + 1])
         ref_words = words[o + 2:o + 2 + counts[j]]
         t = j // nst
-        start = int(enc["tile_off"][t]) + int(enc["soffs"][j])
+        start = int(enc["tile_off"][t]) + int(counts[t * nst:j].sum())
         np.testing.assert_array_equal(enc["words"][start:start + counts[j]], ref_words)
 
 
@@ -139,6 +142,24 @@ def test_encode_rejects_bad_input(rans):
     big = np.random.default_rng(1).integers(-127, 128, size=(16, 65536)).astype(np.int32)
     with pytest.raises(AssertionError):
         rans.encode(big, 16, 65536)
+    # a state's stream beyond 255 words (1024 symbols of ~8 bits each), in
+    # a tile block that itself fits
+    wide = np.random.default_rng(2).integers(-127, 128, size=(16, 4096)).astype(np.int32)
+    with pytest.raises(AssertionError):
+        rans.encode(wide, 16, 4096)
+
+
+def test_stream_lengths_must_match(rans, oracle):
+    codes = oracle.synth_codes(64, 256, 3.0, seed=5)
+    enc = rans.encode(codes, 4, 256, 1)
+    assert enc["slen"][0] > 0
+    bad = dict(enc, slen=enc["slen"].copy())
+    bad["slen"][0] -= 1  # state 1 then starts a word early
+    bad["slen"][1] += 1
+    with pytest.raises(AssertionError):
+        rans.decode_ref(bad)
+    with pytest.raises(AssertionError):
+        oracle.w64_decode(bad)
 
 
 def test_build_table_matches_oracle(rans, oracle, golden):
@@ -191,7 +212,7 @@ def test_bit_accounting(rans, oracle):
     nstates = seqs.shape[0]
     ntiles = (rows // R) * (cols // C)
     pad = len(enc["words"]) - counts.sum()
-    assert enc["bits_state_offs"] == (48 * nstates + 32 * (ntiles + 1) + 16 * pad) / N
+    assert enc["bits_state_offs"] == (40 * nstates + 32 * (ntiles + 1) + 16 * pad) / N
     assert enc["bits_table"] == 32 * 4096 / N
     assert 0 < pad <= 8 * ntiles
     assert np.all(np.diff(enc["tile_off"].astype(np.int64)) % 8 == 0)

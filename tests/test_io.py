@@ -20,7 +20,7 @@ def entries(rans, oracle):
     return out
 
 
-KEYS = ("words", "tile_off", "soffs", "states", "table", "esc_tileptr", "esc_pos", "esc_val")
+KEYS = ("words", "tile_off", "slen", "states", "table", "esc_tileptr", "esc_pos", "esc_val")
 SCALARS = ("R", "C", "S", "shape", "max_tile_words", "max_state_words", "bits_payload",
            "bits_state_offs", "bits_table", "bits_escape")
 

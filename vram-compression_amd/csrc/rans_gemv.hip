@@ -70,7 +70,7 @@ struct WaveLayout {
 struct GemvArgs {
     const uint16_t* words;
     const uint32_t* tile_off;
-    const uint16_t* soffs;
+    const uint8_t* slen;
     const uint32_t* states;
     const uint4* table_lds;  // 2048 x 16 B LDS image of the table
     const int32_t* esc_tileptr;
@@ -90,7 +90,7 @@ struct GemvArgs {
 struct DecodeArgs {
     const uint16_t* words;
     const uint32_t* tile_off;
-    const uint16_t* soffs;
+    const uint8_t* slen;
     const uint32_t* states;
     const uint4* table_lds;
     const int32_t* esc_tileptr;
@@ -250,6 +250,33 @@ __device__ __forceinline__ float wave_transpose_sum(float (&v)[N], int lane) {
 
 constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
 
+// Inclusive prefix sum over the 64 lanes: within each 16-lane row with
+// row_shr 1, 2, 4, 8 (a lane without a source in its row adds 0), then the
+// row totals carried into the rows above with row_bcast 15 and 31.
+__device__ __forceinline__ uint32_t wave_scan(uint32_t v) {
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 to rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 to rows 2, 3
+    return v;
+}
+
+// Word offset of each of the lane's S states within the tile block: the
+// block holds the 64*S streams in state order (j = s*64 + lane), so state
+// j starts after the lengths of states 0..j-1.
+template <int S>
+__device__ __forceinline__ void stream_offsets(const uint32_t (&len)[S], uint32_t (&off)[S]) {
+    uint32_t carry = 0;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const uint32_t inc = wave_scan(len[s]);
+        off[s] = carry + inc - len[s];
+        carry += __builtin_amdgcn_readlane(inc, 63);
+    }
+}
+
 // Per-lane decoder state of S interleaved rANS states, with the table entry
 // of each state's next symbol already read (software pipelined: the read for
 // symbol i+1 is issued before the GEMV work of symbol i).
@@ -339,7 +366,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     const int t = rb * a.ncb + cb;
     // Every kernel argument the prologue needs, fetched in one scalar batch
     // (otherwise each is loaded, and waited for, at its first use).
-    asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.soffs), "s"(a.table_lds),
+    asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.slen), "s"(a.table_lds),
                  "s"(a.words), "s"(a.x), "s"(a.step), "s"(a.esc_tileptr), "s"(a.esc_pos),
                  "s"(a.esc_val), "s"(a.C), "s"(a.cols),
                  "s"(a.L.raw_words), "s"(a.W), "s"(a.ncb), "s"(a.ngroups));
@@ -355,11 +382,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     // This tile's range of the escape side table (lanes 0, 1), also needed early.
     const int tp = a.esc_tileptr[t + min(lane, 1)];
     asm volatile("" ::: "memory");  // keep these two loads first
-    uint32_t st0[S], off0[S];
+    uint32_t st0[S], len0[S];
 #pragma unroll
     for (int s = 0; s < S; s++) {
         st0[s] = a.states[t * nst + 64 * s + lane];
-        off0[s] = a.soffs[t * nst + 64 * s + lane];
+        len0[s] = a.slen[t * nst + 64 * s + lane];
     }
     // x and step for KU column steps are loaded one block ahead of use, so
     // their latency overlaps the decode of the current block.  They are
@@ -478,6 +505,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
 
     {
         Lanes<S> L;
+        uint32_t off0[S];
+        stream_offsets<S>(len0, off0);
         init_lanes<S>(L, tab, raw, st0, off0);
         for (int k0 = 0; k0 < nk; k0 += KU) {
             convert();
@@ -631,18 +660,18 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
     const bool active = t < a.ntiles;
     const int tc = active ? t : a.ntiles - 1;
     const int rb = tc / a.ncb, cb = tc - rb * a.ncb;
-    asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.soffs), "s"(a.table_lds),
+    asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.slen), "s"(a.table_lds),
                  "s"(a.words), "s"(a.step), "s"(a.esc_tileptr), "s"(a.out), "s"(a.C),
                  "s"(a.cols), "s"(a.L.raw_words), "s"(a.W), "s"(a.ncb), "s"(a.ntiles));
 
     const TileOff to = load_tile_off(a.tile_off, tc);
     const int tp = a.esc_tileptr[tc + min(lane, 1)];
     asm volatile("" ::: "memory");  // keep these two loads first
-    uint32_t st0[S], off0[S];
+    uint32_t st0[S], len0[S];
 #pragma unroll
     for (int s = 0; s < S; s++) {
         st0[s] = a.states[tc * nst + 64 * s + lane];
-        off0[s] = a.soffs[tc * nst + 64 * s + lane];
+        len0[s] = a.slen[tc * nst + 64 * s + lane];
     }
     const int nk = a.C / nst;
     const int colbase = cb * a.C + lane;
@@ -671,6 +700,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
     const __amdgpu_buffer_rsrc_t ors =
         __builtin_amdgcn_make_buffer_rsrc(obase, 0, R * a.cols * ESZ, kBufWord3);
     Lanes<S> L;
+    uint32_t off0[S];
+    stream_offsets<S>(len0, off0);
     init_lanes<S>(L, tab, raw, st0, off0);
     // One block of nu <= KU column steps.  The loop below runs whole blocks
     // only (nu = KU, no early exit): exits after 1, 2 or 3 steps' stores
@@ -796,7 +827,7 @@ bool valid_geometry(const rans_w64_matrix* m) {
 }
 
 bool valid_pointers(const rans_w64_matrix* m) {
-    return m->words && m->tile_off && m->soffs && m->states && m->table_lds && m->step &&
+    return m->words && m->tile_off && m->slen && m->states && m->table_lds && m->step &&
            m->esc_tileptr && m->esc_pos && m->esc_val;
 }
 
@@ -927,7 +958,7 @@ int launch_decode_common(const rans_w64_matrix* m, void* out, hipStream_t stream
     DecodeArgs a;
     a.words = m->words;
     a.tile_off = m->tile_off;
-    a.soffs = m->soffs;
+    a.slen = m->slen;
     a.states = m->states;
     a.table_lds = reinterpret_cast<const uint4*>(m->table_lds);
     a.esc_tileptr = m->esc_tileptr;
@@ -980,7 +1011,7 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
     GemvArgs a;
     a.words = m->words;
     a.tile_off = m->tile_off;
-    a.soffs = m->soffs;
+    a.slen = m->slen;
     a.states = m->states;
     a.table_lds = reinterpret_cast<const uint4*>(m->table_lds);
     a.esc_tileptr = m->esc_tileptr;

@@ -23,7 +23,8 @@ constexpr int kEsc = 0;
 struct Encoded {
     std::vector<uint16_t> words;
     std::vector<uint32_t> tile_off;
-    std::vector<uint16_t> soffs;
+    std::vector<uint16_t> soffs;  // stream starts within the tile block (encoder only)
+    std::vector<uint8_t> slen;    // stream lengths, the stored form
     std::vector<uint32_t> states;
     uint32_t table[kM];
     int64_t freq[256];
@@ -135,6 +136,7 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
 
     std::vector<std::vector<uint16_t>> blocks((size_t)ntiles);
     E->soffs.assign((size_t)(ntiles * nst), 0);
+    E->slen.assign((size_t)(ntiles * nst), 0);
     E->states.assign((size_t)(ntiles * nst), 0);
     std::vector<int64_t> payload((size_t)ntiles, 0);
     std::vector<int> too_big((size_t)ntiles, 0);
@@ -172,6 +174,8 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
             const size_t sid = (size_t)(t * nst + j);
             if (blk.size() > 65535) too_big[(size_t)t] = 1;
             E->soffs[sid] = (uint16_t)blk.size();
+            if (cnt > 255) too_big[(size_t)t] = 1;
+            E->slen[sid] = (uint8_t)cnt;
             E->states[sid] = x;
             for (int64_t q = cnt - 1; q >= 0; q--) blk.push_back(emitted[(size_t)q]);
             payload[(size_t)t] += cnt;
@@ -256,7 +260,7 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
 }
 
 extern "C" int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off,
-                                     uint16_t* soffs, uint32_t* states, uint32_t* table,
+                                     uint8_t* slen, uint32_t* states, uint32_t* table,
                                      int64_t* freq, int32_t* esc_tileptr, int32_t* esc_pos,
                                      int32_t* esc_val) {
     if (!handle) return RANS_EARG;
@@ -266,7 +270,7 @@ extern "C" int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* ti
     };
     put(words, E->words);
     put(tile_off, E->tile_off);
-    put(soffs, E->soffs);
+    put(slen, E->slen);
     put(states, E->states);
     put(esc_tileptr, E->esc_tileptr);
     put(esc_pos, E->esc_pos);
@@ -279,7 +283,7 @@ extern "C" int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* ti
 extern "C" void rans_w64_encode_free(void* handle) { delete static_cast<Encoded*>(handle); }
 
 extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
-    if (!m || !out || !m->words || !m->tile_off || !m->soffs || !m->states || !m->table)
+    if (!m || !out || !m->words || !m->tile_off || !m->slen || !m->states || !m->table)
         return RANS_EARG;
     const int32_t rows = m->rows, cols = m->cols, R = m->R, C = m->C, S = m->S;
     if (R <= 0 || C <= 0 || S <= 0 || rows % R || cols % C || C % (64 * S)) return RANS_EGEOMETRY;
@@ -288,11 +292,12 @@ extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
     const int64_t nwords = m->tile_off[ntiles];
     for (int64_t t = 0; t < ntiles; t++) {
         const int32_t rb = (int32_t)(t / ncb), cb = (int32_t)(t % ncb);
+        int64_t start = m->tile_off[t];  // streams follow each other in state order
         for (int32_t j = 0; j < nst; j++) {
             const int32_t s = j / 64, l = j % 64;
             const int64_t sid = t * nst + j;
             uint32_t st = m->states[sid];
-            int64_t p = (int64_t)m->tile_off[t] + m->soffs[sid];
+            int64_t p = start;
             for (int32_t k = 0; k < nk; k++) {
                 const int64_t col = (int64_t)cb * C + 64 * ((int64_t)S * k + s) + l;
                 for (int32_t r = 0; r < R; r++) {
@@ -306,6 +311,9 @@ extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
                 }
             }
             if (st != kRansL) return (int)(sid + 1 > 0x7fffffff ? 0x7fffffff : sid + 1);
+            // the state consumed exactly its stored length
+            if (p - start != m->slen[sid]) return RANS_EARG;
+            start = p;
         }
     }
     // The escape symbol decodes to kEsc-128; the side table must name exactly

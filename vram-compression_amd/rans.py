@@ -51,7 +51,7 @@ class RansMatrixDesc(ctypes.Structure):
                 ("max_tile_words", ctypes.c_int32), ("max_state_words", ctypes.c_int32),
                 ("flags", ctypes.c_int32),
                 ("words", ctypes.c_void_p), ("tile_off", ctypes.c_void_p),
-                ("soffs", ctypes.c_void_p), ("states", ctypes.c_void_p),
+                ("slen", ctypes.c_void_p), ("states", ctypes.c_void_p),
                 ("table", ctypes.c_void_p), ("table_lds", ctypes.c_void_p),
                 ("esc_tileptr", ctypes.c_void_p),
                 ("esc_pos", ctypes.c_void_p), ("esc_val", ctypes.c_void_p),
@@ -184,14 +184,15 @@ def encode(codes, R, C, S=1, threads=None):
     nthreads = threads or min(16, os.cpu_count() or 1)
     rc = lib.rans_w64_encode(_p(codes), rows, cols, R, C, S, nthreads, ctypes.byref(h), _p(info))
     assert rc != -5, "degenerate distribution (single symbol)"
-    assert rc != -6, "a tile needs more than 65535 words: use smaller R or C"
+    assert rc != -6, "a tile needs more than 65535 words, or a state more than 255: " \
+                     "use smaller R or C"
     assert rc != -2, "tile geometry outside the format (R <= 256, C < 2^23)"
     assert rc == 0, f"encode failed ({rc})"
     nwords, ntiles, nstates, nesc, max_tile_words, payload_words, max_state_words = \
         (int(v) for v in info)
     words = np.zeros(nwords, np.uint16)
     tile_off = np.zeros(ntiles + 1, np.uint32)
-    soffs = np.zeros(nstates, np.uint16)
+    slen = np.zeros(nstates, np.uint8)
     states = np.zeros(nstates, np.uint32)
     table = np.zeros(M, np.uint32)
     freq = np.zeros(256, np.int64)
@@ -199,7 +200,7 @@ def encode(codes, R, C, S=1, threads=None):
     esc_pos = np.zeros(nesc, np.int32)
     esc_val = np.zeros(nesc, np.int32)
     try:
-        rc = lib.rans_w64_encode_fetch(h, _p(words), _p(tile_off), _p(soffs), _p(states),
+        rc = lib.rans_w64_encode_fetch(h, _p(words), _p(tile_off), _p(slen), _p(states),
                                        _p(table), _p(freq), _p(esc_tileptr), _p(esc_pos),
                                        _p(esc_val))
         assert rc == 0
@@ -209,12 +210,12 @@ def encode(codes, R, C, S=1, threads=None):
     sym = np.where((codes >= -127) & (codes <= 127), codes + OFFSET, ESC).astype(np.uint8)
     p = freq[sym.ravel()] / M
     pad_words = nwords - payload_words
-    return dict(words=words, tile_off=tile_off, soffs=soffs, states=states, table=table,
+    return dict(words=words, tile_off=tile_off, slen=slen, states=states, table=table,
                 esc_tileptr=esc_tileptr, esc_pos=esc_pos, esc_val=esc_val,
                 R=R, C=C, S=S, shape=codes.shape, max_tile_words=max_tile_words,
                 max_state_words=max_state_words,
                 bits_payload=16 * payload_words / N,
-                bits_state_offs=(48 * nstates + 32 * (ntiles + 1) + 16 * pad_words) / N,
+                bits_state_offs=(40 * nstates + 32 * (ntiles + 1) + 16 * pad_words) / N,
                 bits_table=32 * M / N,
                 bits_escape=32 * (ntiles + 1 + 2 * nesc) / N,
                 entropy_model=float(-np.log2(p).mean()))
@@ -271,7 +272,7 @@ def pick_tiling(rows, cols, R=None, S=1, target_states=None):
 def _host_desc(enc, keep):
     """rans_w64_matrix over host numpy arrays (for rans_w64_decode_host)."""
     arrs = {k: np.ascontiguousarray(enc[k]) for k in
-            ("words", "tile_off", "soffs", "states", "table", "esc_tileptr", "esc_pos", "esc_val")}
+            ("words", "tile_off", "slen", "states", "table", "esc_tileptr", "esc_pos", "esc_val")}
     keep.append(arrs)
     rows, cols = enc["shape"]
     d = RansMatrixDesc(rows=rows, cols=cols, R=enc["R"], C=enc["C"], S=enc["S"],
@@ -325,7 +326,7 @@ class RansMatrix:
 
         self.words = up(enc["words"], np.int16)
         self.tile_off = up(enc["tile_off"], np.int32)
-        self.soffs = up(enc["soffs"], np.int16)
+        self.slen = up(enc["slen"], np.uint8)
         self.states = up(enc["states"], np.int32)
         # the kernels read the table's LDS image; the packed table is only
         # for the host decoder and stays on the host
@@ -344,7 +345,7 @@ class RansMatrix:
             max_tile_words=self.max_tile_words, max_state_words=self.max_state_words,
             flags=(int(flags) & F_WORDS_MASK) | (0 if len(enc["esc_pos"]) else F_NO_ESCAPES),
             words=self.words.data_ptr(), tile_off=self.tile_off.data_ptr(),
-            soffs=self.soffs.data_ptr(), states=self.states.data_ptr(),
+            slen=self.slen.data_ptr(), states=self.states.data_ptr(),
             table=None, table_lds=self.table_lds.data_ptr(),
             esc_tileptr=self.esc_tileptr.data_ptr(),
             esc_pos=self.esc_pos.data_ptr(), esc_val=self.esc_val.data_ptr(),
@@ -353,7 +354,7 @@ class RansMatrix:
         self._ensure_workspace(4)
         # device bytes (the 32 KB table image in place of the 16 KB table)
         self.nbytes = sum(t.numel() * t.element_size() for t in
-                          (self.words, self.tile_off, self.soffs, self.states, self.table_lds,
+                          (self.words, self.tile_off, self.slen, self.states, self.table_lds,
                            self.esc_tileptr)) + 8 * int(len(enc["esc_pos"]))
 
     def tune(self, batch=1, x_dtype=torch.bfloat16, iters=20):

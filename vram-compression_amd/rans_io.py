@@ -9,7 +9,8 @@ Layout (all integers little endian, every section 64-byte aligned):
 
     header, 64 bytes
         magic      8 bytes  b"VRAMCW64"
-        version    u32      2 (1 held a row-CSR side table; it is not read)
+        version    u32      3 (1 and 2 held a row-CSR side table or 16-bit
+                            stream offsets; they are not read)
         nmat       u32      number of matrices
         index_off  u64      byte offset of the index
         file_bytes u64      total file size (truncation check)
@@ -19,12 +20,12 @@ Layout (all integers little endian, every section 64-byte aligned):
         rows, cols, R, C, S, max_tile_words, max_state_words, flags   i32 x 8
         nwords, ntiles, nstates, nesc, payload_words                  u64 x 5
         entropy_model                                                 f64
-        offsets of words, tile_off, soffs, states, table, esc_tileptr,
+        offsets of words, tile_off, slen, states, table, esc_tileptr,
                    esc_pos, esc_val, step                             u64 x 9
         crc32 of the nine sections, in that order                     u32
         zero padding to 256 bytes
     sections
-        words u16[nwords], tile_off u32[ntiles+1], soffs u16[nstates],
+        words u16[nwords], tile_off u32[ntiles+1], slen u8[nstates],
         states u32[nstates], table u32[4096] (reference packing),
         esc_tileptr i32[ntiles+1], esc_pos i32[nesc], esc_val i32[nesc],
         step f32[cols]
@@ -41,12 +42,12 @@ import numpy as np
 import rans
 
 MAGIC = b"VRAMCW64"
-VERSION = 2
+VERSION = 3
 _HEADER = struct.Struct("<8sIIQQ32x")
 _RECORD = struct.Struct("<64s8i5Qd9QI")
 RECORD_BYTES = 256
 ALIGN = 64
-_SECTIONS = (("words", np.uint16), ("tile_off", np.uint32), ("soffs", np.uint16),
+_SECTIONS = (("words", np.uint16), ("tile_off", np.uint32), ("slen", np.uint8),
              ("states", np.uint32), ("table", np.uint32), ("esc_tileptr", np.int32),
              ("esc_pos", np.int32), ("esc_val", np.int32), ("step", np.float32))
 assert _HEADER.size == 64 and _RECORD.size <= RECORD_BYTES
@@ -57,7 +58,7 @@ def _align(n):
 
 
 def _section_lengths(rows, cols, nwords, ntiles, nstates, nesc):
-    return dict(words=nwords, tile_off=ntiles + 1, soffs=nstates, states=nstates,
+    return dict(words=nwords, tile_off=ntiles + 1, slen=nstates, states=nstates,
                 table=rans.M, esc_tileptr=ntiles + 1, esc_pos=nesc, esc_val=nesc, step=cols)
 
 
@@ -161,13 +162,13 @@ def load(path, verify=True, mmap=True):
             raise ValueError(f"{name}: CRC mismatch (file corrupted)")
         N = rows * cols
         pad = nwords - payload_words
-        enc = dict(words=arrays["words"], tile_off=arrays["tile_off"], soffs=arrays["soffs"],
+        enc = dict(words=arrays["words"], tile_off=arrays["tile_off"], slen=arrays["slen"],
                    states=arrays["states"], table=arrays["table"],
                    esc_tileptr=arrays["esc_tileptr"], esc_pos=arrays["esc_pos"],
                    esc_val=arrays["esc_val"], R=R, C=C, S=S, shape=(rows, cols),
                    max_tile_words=mtw, max_state_words=msw,
                    bits_payload=16 * payload_words / N,
-                   bits_state_offs=(48 * nstates + 32 * (ntiles + 1) + 16 * pad) / N,
+                   bits_state_offs=(40 * nstates + 32 * (ntiles + 1) + 16 * pad) / N,
                    bits_table=32 * rans.M / N,
                    bits_escape=32 * (ntiles + 1 + 2 * nesc) / N,
                    entropy_model=entropy_model)
