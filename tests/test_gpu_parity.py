@@ -343,3 +343,46 @@ def test_few_column_tiles(rans, oracle, lib, dev, rows, cols, R, C):
         ys.append((y4, y3, y1))
     for a, b in zip(*ys):
         assert torch.equal(a, b)
+
+
+def test_random_geometries(rans, oracle, lib, dev):
+    """Seeded random tile geometries over every compiled R and S (columns
+    per tile a random multiple of 64*S, several tile rows and columns),
+    codes at a random rate with ~0.5% escapes: codes bit-exact, bf16
+    decode bit-exact, GEMV against the float64 oracle at a random batch
+    with bf16 or f32 x, both word-fetch policies bitwise equal."""
+    rng = np.random.default_rng(2024)
+    for case in range(24):
+        R = int(rng.choice([1, 2, 3, 4, 8, 16]))
+        S = int(rng.choice([1, 2, 4]))
+        C = 64 * S * int(rng.integers(1, 5))
+        rows = R * int(rng.integers(1, 9))
+        cols = C * int(rng.integers(1, 11))
+        bits = float(rng.uniform(1.5, 6.0))
+        batch = int(rng.integers(1, 7))
+        f32 = bool(rng.integers(0, 2))
+        print(f"case random {case}: {rows}x{cols} R={R} C={C} S={S} bits={bits:.2f} "
+              f"batch={batch} f32={f32}", flush=True)
+        codes = oracle.synth_codes(rows, cols, bits, seed=case)
+        codes[0, 0], codes[-1, -1] = 7, -7  # at least two symbols, even in a tiny matrix
+        hit = rng.random(codes.shape) < 0.005
+        codes[hit] = rng.integers(128, 3000, size=int(hit.sum())) * rng.choice([-1, 1], int(hit.sum()))
+        step = (rng.random(cols) + 0.25).astype(np.float32)
+        enc = rans.encode(codes, R, C, S)
+        x = torch.from_numpy(rng.standard_normal((batch, cols)).astype(np.float32)).cuda()
+        if not f32:
+            x = x.bfloat16()
+        ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64),
+                              step.astype(np.float64))
+        ys = []
+        for flags in (rans.F_WORDS_ALWAYS, rans.F_WORDS_REFILL):
+            m = rans.RansMatrix(enc, torch.from_numpy(step), lib, flags=flags)
+            np.testing.assert_array_equal(m.decode_codes().cpu().numpy(), codes)
+            y = m.gemv(x).cpu()
+            for b in range(batch):
+                assert _rel_l2(y[b].numpy(), ref[b]) <= REL_L2, (case, b)
+            ys.append(y)
+        assert torch.equal(ys[0], ys[1])
+        dec = m.decode().cpu()
+        want = (torch.from_numpy(codes.astype(np.float32)) * torch.from_numpy(step)).bfloat16()
+        assert torch.equal(dec.view(torch.int16), want.view(torch.int16))
