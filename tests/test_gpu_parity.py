@@ -129,7 +129,7 @@ def test_split_k_deterministic(rans, oracle, lib, dev):
         assert _rel_l2(ys[0], ref) <= REL_L2
 
 
-@pytest.mark.parametrize("batch", [1, 3, 4, 5])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 6, 7])
 def test_batch(rans, oracle, lib, dev, batch):
     rows, cols = 512, 2048
     print(f"case batch {batch}", flush=True)

@@ -83,6 +83,9 @@ struct GemvArgs {
     uint32_t* counters;  // [rows/R]
     int rows, cols, C, ncb, ngroups;
     int W;        // waves per workgroup (= blockDim.x / 64, as a kernel argument)
+    int nb;       // x/y rows of this launch, 1..B: a batch-4 kernel also runs a
+                  // remainder of 2 or 3 (its other rows re-read the last x row
+                  // and store nothing)
     int has_esc;  // 0: the side table is empty
     WaveLayout L;
 };
@@ -369,7 +372,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.slen), "s"(a.table_lds),
                  "s"(a.words), "s"(a.x), "s"(a.step), "s"(a.esc_tileptr), "s"(a.esc_pos),
                  "s"(a.esc_val), "s"(a.C), "s"(a.cols),
-                 "s"(a.L.raw_words), "s"(a.W), "s"(a.ncb), "s"(a.ngroups));
+                 "s"(a.L.raw_words), "s"(a.W), "s"(a.ncb), "s"(a.ngroups), "s"(a.nb));
 
     // Everything the wave needs from memory before decoding is requested in
     // one batch: initial states, stream offsets, the first block of x and
@@ -401,8 +404,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
 #pragma unroll
     for (int b = 0; b < B; b++)
         xrs[b] = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(static_cast<const uint8_t*>(a.x)) + (size_t)b * a.cols * XS, 0,
-            a.cols * XS, kBufWord3);
+            const_cast<uint8_t*>(static_cast<const uint8_t*>(a.x)) + (size_t)min(b, a.nb - 1) * a.cols * XS,
+            0, a.cols * XS, kBufWord3);
     const __amdgpu_buffer_rsrc_t srs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.step), 0, a.cols * 4, kBufWord3);
     // bf16 values kept as __bf16 (an integer register pin would be widened
@@ -499,7 +502,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
             esr[p] = __float_as_uint(a.step[col]);
 #pragma unroll
             for (int b = 0; b < B; b++)
-                exr[p][b] = load_x_bits(a.x, (int64_t)b * a.cols + col, XBF16);
+                exr[p][b] = load_x_bits(a.x, (int64_t)min(b, a.nb - 1) * a.cols + col, XBF16);
         }
     };
 
@@ -564,7 +567,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         const int col = esc_col(pos);
         const float ve = e < e_hi ? (float)a.esc_val[ec] * a.step[col] : 0.f;
 #pragma unroll
-        for (int b = 0; b < B; b++) ev[b] = ve * load_x(a.x, (int64_t)b * a.cols + col, XBF16);
+        for (int b = 0; b < B; b++)
+            ev[b] = ve * load_x(a.x, (int64_t)min(b, a.nb - 1) * a.cols + col, XBF16);
         add_escape<R, B>(acc, pos & 0xFF, ev);
     }
 
@@ -600,7 +604,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         for (int ww = 0; ww < W; ww++) v += red[ww * (R * B) + tid];
     }
     if (a.ngroups == 1) {
-        if (tid < R * B) a.y[(int64_t)b * a.rows + row] = v;
+        if (tid < R * B && b < a.nb) a.y[(int64_t)b * a.rows + row] = v;
         return;
     }
 
@@ -629,7 +633,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
             for (int gg = 0; gg < a.ngroups; gg++)
                 s += __hip_atomic_load(&a.partial[((int64_t)gg * B + b) * a.rows + row],
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            a.y[(int64_t)b * a.rows + row] = s;
+            if (b < a.nb) a.y[(int64_t)b * a.rows + row] = s;
         }
         if (tid == 0)
             __hip_atomic_store(&a.counters[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -986,7 +990,7 @@ extern "C" int64_t rans_gemv_workspace_bytes(const rans_w64_matrix* m, int batch
     if (!waves) return RANS_EGEOMETRY;
     const int ngroups = (m->cols / m->C) / waves;
     if (ngroups <= 1) return 0;
-    const int bmax = batch >= 4 ? 4 : 1;
+    const int bmax = batch >= 2 ? 4 : 1;  // 2 or more run the batch-4 kernel
     return (int64_t)counters_bytes(m) + (int64_t)ngroups * bmax * m->rows * 4;
 }
 
@@ -1033,15 +1037,18 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
     const size_t lds = lds_bytes(waves, a.L);
     const int grid = (m->rows / m->R) * ngroups;
 
-    // Batches run in chunks of 4 vectors, the remainder one vector at a time.
+    // Batches run in chunks of up to 4 vectors on the batch-4 kernel, a
+    // single remaining vector on the batch-1 kernel.
     int done = 0;
     while (done < batch) {
-        const int B = batch - done >= 4 ? 4 : 1;
+        const int nb = batch - done >= 4 ? 4 : batch - done;
+        const int B = nb >= 2 ? 4 : 1;
         a.x = static_cast<const uint8_t*>(x) + (size_t)done * m->cols * xsz;
         a.y = static_cast<float*>(y) + (size_t)done * m->rows;
+        a.nb = nb;
         const int rc = dispatch_gemv(a, m->R, m->S, B, var, waves, lds, grid, stream);
         if (rc != 0) return rc;
-        done += B;
+        done += nb;
     }
     return 0;
 }

@@ -2,9 +2,10 @@
 
 The reference names model integration as its next step (README.md:39) and
 stops at the kernel.  RansLinear is that step: forward(x) runs the fused
-decode+GEMV kernel for decode-sized batches and, for large batches
-(prefill), decodes the weight to bf16 once and calls the dense GEMM, which
-is then the faster path.  Inference only: the weight is not a parameter.
+decode+GEMV kernel for decode-sized batches (up to 8 rows) and, for larger
+batches (prefill), decodes the weight to bf16 once and calls the dense GEMM,
+which is then the faster path.  Inference only: the weight is not a
+parameter.
 
 quantize_uniform is a plain uniform quantiser (one step per tensor, chosen
 for a target code entropy) so that ordinary nn.Linear layers can be
@@ -16,7 +17,11 @@ import torch
 
 import rans
 
-PREFILL_ROWS = 16  # batches above this decode the weight and use the dense GEMM
+# Batches above this decode the weight to bf16 and use the dense GEMM.  The
+# fused GEMV runs 4 vectors per launch, so its time grows with the batch
+# while decode+GEMM stays flat; on MI355X the fused path wins up to 8 rows
+# on 1536x1536 to 25600x5120 matrices and loses from about 12.
+PREFILL_ROWS = 8
 
 
 def _entropy(codes):
