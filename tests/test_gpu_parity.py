@@ -386,3 +386,44 @@ def test_random_geometries(rans, oracle, lib, dev):
         dec = m.decode().cpu()
         want = (torch.from_numpy(codes.astype(np.float32)) * torch.from_numpy(step)).bfloat16()
         assert torch.equal(dec.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("rows,cols,C,batch", [
+    (35, 192, 192, 4),         # one tile, one wave: 140 (row, batch) sums for 64 threads
+    (70, 384, 192, 4),         # two waves per workgroup
+    (105, 1024, 64, 3),        # 16 column tiles: two column groups (split reduction)
+    (140, 576, 64, 1),         # 9 column tiles: three waves, three groups
+    (8960, 1536, 192, 1),      # Qwen2.5-1.5B gate/up: 2048 tiles of 35 x 192
+])
+def test_r35_tiles(rans, oracle, lib, dev, rows, cols, C, batch):
+    """Tiles of 35 rows (one state per lane): codes bit-exact, bf16 decode
+    bit-exact, GEMV against the float64 oracle with ~0.2% escapes, for both
+    word-fetch policies (bitwise equal), at batch 1, 3 and 4; R=35 with two
+    states per lane has no kernel and is refused."""
+    print(f"case r35 {rows}x{cols} C={C} batch={batch}", flush=True)
+    rng = np.random.default_rng(rows + cols)
+    codes = oracle.synth_codes(rows, cols, 3.25, seed=rows)
+    codes[0, 0], codes[-1, -1] = 5, -5
+    hit = rng.random(codes.shape) < 0.002
+    codes[hit] = rng.integers(128, 900, size=int(hit.sum())) * rng.choice([-1, 1], int(hit.sum()))
+    step = (rng.random(cols) + 0.25).astype(np.float32)
+    assert rans.pick_tiling(8960, 1536) == (35, 192)
+    enc = rans.encode(codes, 35, C, 1)
+    x = torch.from_numpy(rng.standard_normal((batch, cols)).astype(np.float32)).cuda().bfloat16()
+    ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64), step.astype(np.float64))
+    ys = []
+    for flags in (rans.F_WORDS_ALWAYS, rans.F_WORDS_REFILL):
+        m = rans.RansMatrix(enc, torch.from_numpy(step), lib, flags=flags)
+        np.testing.assert_array_equal(m.decode_codes().cpu().numpy(), codes)
+        y = m.gemv(x).cpu()
+        for b in range(batch):
+            assert _rel_l2(y[b].numpy(), ref[b]) <= REL_L2, (flags, b)
+        ys.append(y)
+    assert torch.equal(ys[0], ys[1])
+    dec = m.decode().cpu()
+    want = (torch.from_numpy(codes.astype(np.float32)) * torch.from_numpy(step)).bfloat16()
+    assert torch.equal(dec.view(torch.int16), want.view(torch.int16))
+    if cols % 128 == 0 and C % 128 == 0:
+        m2 = rans.RansMatrix(rans.encode(codes, 35, C, 2), torch.from_numpy(step), lib)
+        with pytest.raises(AssertionError, match="HIP error -1"):
+            m2.gemv(x)

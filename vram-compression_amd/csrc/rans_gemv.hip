@@ -36,7 +36,6 @@ namespace {
 constexpr uint32_t kProbM = 4096;
 constexpr uint32_t kRansL = 1u << 16;
 constexpr int kMaxWaves = 8;
-constexpr int kMaxRB = 64;  // largest R*B compiled (16 * 4)
 
 // Table entry in LDS: {freq | code<<24, slot - cum}; one mad consumes both
 // words and the code is the sign-extended top byte.
@@ -44,8 +43,13 @@ using TabEntry = uint2;
 
 // LDS: the expanded table and the reduction scratch are static __shared__
 // arrays (their offsets are compile-time constants, so table addressing
-// needs no base add); the per-wave regions are dynamic.
-constexpr int kStaticLds = (int)sizeof(TabEntry) * (int)kProbM + 4 * kMaxWaves * kMaxRB + 16;
+// needs no base add); the per-wave regions are dynamic.  The GEMV's
+// reduction scratch holds R*B floats per wave: the host reserves it for a
+// batch of 4 (the largest compiled), plus the 16-byte arrival flag.
+constexpr int gemv_static_lds(int R) {
+    return (int)sizeof(TabEntry) * (int)kProbM + 4 * kMaxWaves * R * 4 + 16;
+}
+constexpr int kDecodeStaticLds = (int)sizeof(TabEntry) * (int)kProbM;
 constexpr int kLdsMax = 160 * 1024;
 constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3 for gfx9 raw loads
 
@@ -253,6 +257,23 @@ __device__ __forceinline__ float wave_transpose_sum(float (&v)[N], int lane) {
 
 constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
 
+// Sums each of the N values w[OFF..OFF+N) over the 64 lanes into
+// out[OFF..OFF+N), for any N: power-of-two chunks of at most 64 values,
+// largest first (35 = 32 + 2 + 1), each through wave_transpose_sum.
+template <int OFF, int N, int NT>
+__device__ __forceinline__ void transpose_sum_store(const float (&w)[NT], float* out, int lane) {
+    if constexpr (N > 0) {
+        constexpr int C = N >= 64 ? 64 : 1 << ilog2(N);
+        float v[C];
+#pragma unroll
+        for (int i = 0; i < C; i++) v[i] = w[OFF + i];
+        const float t = wave_transpose_sum<C>(v, lane);
+        constexpr int sh = 6 - ilog2(C);
+        if ((lane & ((1 << sh) - 1)) == 0) out[OFF + (lane >> sh)] = t;
+        transpose_sum_store<OFF + C, N - C, NT>(w, out, lane);
+    }
+}
+
 // Inclusive prefix sum over the 64 lanes: within each 16-lane row with
 // row_shr 1, 2, 4, 8 (a lane without a source in its row adds 0), then the
 // row totals carried into the rows above with row_bcast 15 and 31.
@@ -354,7 +375,7 @@ __device__ __forceinline__ void add_escape(float (&acc)[R][B], int re, const flo
 template <int R, int S, int B, bool XBF16, bool REFILL>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs a) {
     __shared__ __align__(16) TabEntry tab[kProbM];
-    __shared__ float red[kMaxWaves * kMaxRB];
+    __shared__ float red[kMaxWaves * R * B];
     __shared__ int flag[4];
     extern __shared__ __align__(16) uint16_t dyn[];
     constexpr int nst = 64 * S;
@@ -573,15 +594,13 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     }
 
     constexpr int NRB = R * B;
-    if constexpr (NRB >= 8 && (NRB & (NRB - 1)) == 0) {
+    if constexpr (NRB >= 8) {
         float w[NRB];
 #pragma unroll
         for (int r = 0; r < R; r++)
 #pragma unroll
             for (int b = 0; b < B; b++) w[r * B + b] = acc[r][b];
-        const float v = wave_transpose_sum<NRB>(w, lane);
-        constexpr int sh = 6 - ilog2(NRB);
-        if ((lane & ((1 << sh) - 1)) == 0) red[wave * NRB + (lane >> sh)] = v;
+        transpose_sum_store<0, NRB, NRB>(w, red + wave * NRB, lane);
     } else {
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -594,17 +613,20 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     }
     __syncthreads();
 
+    // Per (row, batch) totals over the workgroup's waves, entry i = r*B + b.
+    // R*B can exceed the workgroup's threads (R = 35 at batch 4).
     const int tid = threadIdx.x;
-    float v = 0.f;
-    int row = 0, b = 0;
-    if (tid < R * B) {
-        const int r = tid / B;
-        b = tid - r * B;
-        row = rb * R + r;
-        for (int ww = 0; ww < W; ww++) v += red[ww * (R * B) + tid];
-    }
+    const int nthr = 64 * W;
+    auto total = [&](int i) {
+        float v = 0.f;
+        for (int ww = 0; ww < W; ww++) v += red[ww * NRB + i];
+        return v;
+    };
     if (a.ngroups == 1) {
-        if (tid < R * B && b < a.nb) a.y[(int64_t)b * a.rows + row] = v;
+        for (int i = tid; i < NRB; i += nthr) {
+            const int r = i / B, b = i - r * B;
+            if (b < a.nb) a.y[(int64_t)b * a.rows + rb * R + r] = total(i);
+        }
         return;
     }
 
@@ -616,9 +638,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     // the last workgroup reads the partials with agent-scope (coherent)
     // loads.  This avoids release/acquire fences, which on this chip write
     // back or invalidate the whole L2 of the XCD.
-    if (tid < R * B)
-        __hip_atomic_store(&a.partial[((int64_t)g * B + b) * a.rows + row], v, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = tid; i < NRB; i += nthr) {
+        const int r = i / B, b = i - r * B;
+        __hip_atomic_store(&a.partial[((int64_t)g * B + b) * a.rows + rb * R + r], total(i),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
@@ -628,12 +652,13 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     }
     __syncthreads();
     if (*flag) {
-        if (tid < R * B) {
+        for (int i = tid; i < NRB; i += nthr) {
+            const int r = i / B, b = i - r * B;
             float s = 0.f;
             for (int gg = 0; gg < a.ngroups; gg++)
-                s += __hip_atomic_load(&a.partial[((int64_t)gg * B + b) * a.rows + row],
+                s += __hip_atomic_load(&a.partial[((int64_t)gg * B + b) * a.rows + rb * R + r],
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (b < a.nb) a.y[(int64_t)b * a.rows + row] = s;
+            if (b < a.nb) a.y[(int64_t)b * a.rows + rb * R + r] = s;
         }
         if (tid == 0)
             __hip_atomic_store(&a.counters[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -841,14 +866,14 @@ int gemv_waves(const rans_w64_matrix* m) {
     const int ncb = m->cols / m->C;
     const WaveLayout L = wave_layout(m);
     for (int w = kMaxWaves; w >= 1; w--)
-        if (ncb % w == 0 && lds_bytes(w, L) + kStaticLds <= (size_t)kLdsMax) return w;
+        if (ncb % w == 0 && lds_bytes(w, L) + gemv_static_lds(m->R) <= (size_t)kLdsMax) return w;
     return 0;
 }
 
 int decode_waves(const rans_w64_matrix* m) {
     const WaveLayout L = wave_layout(m);
     for (int w = 4; w >= 1; w >>= 1)
-        if (lds_bytes(w, L) + kStaticLds <= (size_t)kLdsMax) return w;
+        if (lds_bytes(w, L) + kDecodeStaticLds <= (size_t)kLdsMax) return w;
     return 0;
 }
 
@@ -856,18 +881,19 @@ size_t counters_bytes(const rans_w64_matrix* m) {
     return (((size_t)(m->rows / m->R) * 4 + 255) / 256) * 256;
 }
 
-// Opt in to more than 64 KB of dynamic LDS once per kernel.
+// Opt in to more than 64 KB of LDS once per kernel (bytes dynamic, plus
+// static_bytes or more of static __shared__ arrays).
 std::mutex g_attr_mu;
 const void* g_attr_done[512];
 int g_attr_n = 0;
 
-hipError_t ensure_lds(const void* fn, size_t bytes) {
-    if (bytes + kStaticLds <= 65536) return hipSuccess;
+hipError_t ensure_lds(const void* fn, size_t bytes, int static_bytes) {
+    if (bytes + static_bytes <= 65536) return hipSuccess;
     std::lock_guard<std::mutex> lk(g_attr_mu);
     for (int i = 0; i < g_attr_n; i++)
         if (g_attr_done[i] == fn) return hipSuccess;
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       kLdsMax - kStaticLds);
+                                       kLdsMax - static_bytes);
     if (e == hipSuccess && g_attr_n < 512) g_attr_done[g_attr_n++] = fn;
     return e;
 }
@@ -875,7 +901,7 @@ hipError_t ensure_lds(const void* fn, size_t bytes) {
 template <int R, int S, int B, bool XBF16, bool REFILL>
 int launch_gemv_t(const GemvArgs& a, int waves, size_t lds, int grid, hipStream_t stream) {
     const void* fn = reinterpret_cast<const void*>(&rans_w64_gemv_kernel<R, S, B, XBF16, REFILL>);
-    hipError_t e = ensure_lds(fn, lds);
+    hipError_t e = ensure_lds(fn, lds, gemv_static_lds(R));
     if (e != hipSuccess) return (int)e;
     hipLaunchKernelGGL((rans_w64_gemv_kernel<R, S, B, XBF16, REFILL>), dim3(grid), dim3(64 * waves),
                        lds, stream, a);
@@ -922,18 +948,23 @@ int dispatch_gemv(const GemvArgs& a, int R, int S, int B, int var, int waves, si
         case 4: return dispatch_s<4>(a, S, B, var, waves, lds, grid, st);
         case 8: return dispatch_s<8>(a, S, B, var, waves, lds, grid, st);
         case 16: return dispatch_s<16>(a, S, B, var, waves, lds, grid, st);
+        case 35: return S == 1 ? dispatch_b<35, 1>(a, B, var, waves, lds, grid, st) : RANS_EUNSUPPORTED;
         default: return RANS_EUNSUPPORTED;
     }
 }
 
+// R = 35 (one state per lane only) splits rows of 8960 = 256 x 35 into 256
+// tile rows, so that 8960 x 1536 (Qwen2.5-1.5B's gate and up projections)
+// runs as 2048 tiles of 35 x 192: two waves on every SIMD.
 bool supported_rs(int R, int S) {
-    return (R == 1 || R == 2 || R == 3 || R == 4 || R == 8 || R == 16) && (S == 1 || S == 2 || S == 4);
+    return ((R == 1 || R == 2 || R == 3 || R == 4 || R == 8 || R == 16) && (S == 1 || S == 2 || S == 4)) ||
+           (R == 35 && S == 1);
 }
 
 template <int R, int S, int MODE>
 int launch_decode_t(const DecodeArgs& a, int waves, size_t lds, int grid, hipStream_t stream) {
     const void* fn = reinterpret_cast<const void*>(&rans_w64_decode_kernel<R, S, MODE>);
-    hipError_t e = ensure_lds(fn, lds);
+    hipError_t e = ensure_lds(fn, lds, kDecodeStaticLds);
     if (e != hipSuccess) return (int)e;
     hipLaunchKernelGGL((rans_w64_decode_kernel<R, S, MODE>), dim3(grid), dim3(64 * waves), lds,
                        stream, a);
@@ -947,6 +978,7 @@ int dispatch_decode(const DecodeArgs& a, int R, int S, int waves, size_t lds, in
     if (R == RR && S == SS) return launch_decode_t<RR, SS, MODE>(a, waves, lds, grid, st);
 #define VRAMC_DEC_R(RR) VRAMC_DEC_CASE(RR, 1) VRAMC_DEC_CASE(RR, 2) VRAMC_DEC_CASE(RR, 4)
     VRAMC_DEC_R(1) VRAMC_DEC_R(2) VRAMC_DEC_R(3) VRAMC_DEC_R(4) VRAMC_DEC_R(8) VRAMC_DEC_R(16)
+    VRAMC_DEC_CASE(35, 1)
 #undef VRAMC_DEC_R
 #undef VRAMC_DEC_CASE
     return RANS_EUNSUPPORTED;

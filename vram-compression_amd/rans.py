@@ -38,6 +38,8 @@ X_F32, X_BF16 = 0, 1
 # rans_w64_matrix.flags: word fetch of the GEMV (0 = library default), and
 # the empty-side-table promise (set by RansMatrix itself)
 F_WORDS_ALWAYS, F_WORDS_REFILL, F_WORDS_MASK, F_NO_ESCAPES = 1, 2, 3, 4
+# tile heights with compiled kernels; 35 only with one state per lane
+SUPPORTED_R = (35, 16, 8, 4, 3, 2, 1)
 
 HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared",
                # packed fp32 VALU ops stay disabled on this platform
@@ -223,7 +225,9 @@ def encode(codes, R, C, S=1, threads=None):
 
 def pick_tiling(rows, cols, R=None, S=1, target_states=None):
     """A legal (R, C) for the w64 format: C a multiple of 64*S dividing cols,
-    R in {1, 2, 3, 4, 8, 16}.  Chosen by measurement on MI355X:
+    R in {1, 2, 3, 4, 8, 16}, or 35 at S=1 (rows of 8960 = 256 x 35: 8960 x
+    1536 becomes 2048 tiles of 35 x 192, two waves on every SIMD).  Chosen by
+    measurement on MI355X:
 
     - states: about 105 symbols per state for mid-size matrices (at
       1536x8960 that is 2048 waves, two per SIMD: two waves on a SIMD slow
@@ -242,7 +246,7 @@ def pick_tiling(rows, cols, R=None, S=1, target_states=None):
     nst = 64 * S
     cands = [c for c in range(nst, cols + 1, nst) if cols % c == 0]
     assert cands, f"cols={cols} has no divisor that is a multiple of {nst}"
-    Rs = [R] if R else [r for r in (16, 8, 4, 3, 2, 1) if rows % r == 0]
+    Rs = [R] if R else [r for r in (SUPPORTED_R if S == 1 else SUPPORTED_R[1:]) if rows % r == 0]
     n = rows * cols
     if target_states:
         target = target_states
