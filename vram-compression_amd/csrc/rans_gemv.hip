@@ -17,12 +17,14 @@
 //   4. each lane runs S independent rANS states; per column step a lane
 //      loads x[c]*step[c] once (the waterfilling fold happens here, one block
 //      of column steps ahead of use) and reuses it for the R rows of the tile;
-//   5. row sums are reduced across the 64 lanes with cross-lane shuffles and
-//      across the W waves through LDS in a fixed order, each wave adds its
-//      tile's escapes from the side table, and y is written; when one workgroup does not
-//      cover all column tiles, partial sums go to a workspace and the last
-//      workgroup of the tile row adds them up in a fixed order (no atomics on
-//      y, no memset, deterministic).
+//   5. each wave adds its tile's escapes from the side table (into the
+//      accumulators before the reduction, or for 35-row tiles into the
+//      reduced sums with LDS float adds); row sums are reduced across the 64
+//      lanes with a transpose-reduce (permlane swaps and DPP) and across the
+//      W waves through LDS in a fixed order, and y is written.  When one
+//      workgroup does not cover all column tiles, partial sums go to a
+//      workspace and the last workgroup of the tile row adds them up in a
+//      fixed order (no atomics on y, no memset, deterministic).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
