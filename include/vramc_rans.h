@@ -118,6 +118,18 @@ int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_dtype, int b
  * that must be zero before the first launch; the kernel leaves them zero. */
 int64_t rans_gemv_workspace_bytes(const rans_w64_matrix* m, int batch);
 
+/* launch_rans_gemv for n <= 4 matrices that share x, in one launch:
+ * ys[i] (batch x ms[i]->rows f32) gets ms[i]'s product.  No reference
+ * counterpart: it is for projections that read the same activations (a
+ * layer's q, k and v, or its gate and up), whose separate GEMVs each leave
+ * most of the chip idle.  The matrices must have the same cols, R and S = 1,
+ * and one workgroup per tile row (cols/C equal to the waves per workgroup,
+ * the same for all: cols/C <= 8 and the tile block within LDS); otherwise
+ * RANS_EUNSUPPORTED (or RANS_EGEOMETRY) and nothing is launched.  Results
+ * are bitwise those of separate launch_rans_gemv calls. */
+int launch_rans_gemv_group(const rans_w64_matrix* const* ms, int n, const void* x, int x_dtype,
+                           int batch, float* const* ys, hipStream_t stream);
+
 /* Decode to a dense bf16 matrix out[r,c] = bf16(code[r,c]*step[c]) (round to
  * nearest even).  Replaces launch_rans_decode (rans_gemv.cu:155-162). */
 int launch_rans_decode(const rans_w64_matrix* m, void* out_bf16, hipStream_t stream);

@@ -74,6 +74,32 @@ def test_argument_validation_without_gpu(rans, lib):
     assert lib.launch_int4_gemv(x, x, y, 4, 48, None) == -2
 
 
+def test_group_validation_without_gpu(rans, lib):
+    """launch_rans_gemv_group refuses, before any launch, what one launch
+    cannot run: no matrices, more than 4, different cols or R, two states
+    per lane, or split-K tilings."""
+    x = ctypes.c_void_p(0x2000)
+
+    def call(descs, n=None, ys=None):
+        arr = (ctypes.c_void_p * max(1, len(descs)))(*[ctypes.addressof(d) for d in descs])
+        yarr = (ctypes.c_void_p * max(1, len(descs)))(*([0x3000] * len(descs) if ys is None else ys))
+        return lib.launch_rans_gemv_group(arr, len(descs) if n is None else n, x, 0, 1, yarr, None)
+
+    a = _desc(rans, cols=2048)  # 8 column tiles: one workgroup per tile row
+    b = _desc(rans, rows=512, cols=2048)
+    assert lib.launch_rans_gemv_group(None, 2, x, 0, 1, None, None) == -4
+    assert call([a, b], n=0) == -4
+    assert call([a] * 5) == -1
+    assert call([a, _desc(rans, cols=4096, C=512)]) == -1  # different cols
+    assert call([a, _desc(rans, rows=256, cols=2048, R=16)]) == -1  # different R
+    assert call([_desc(rans, cols=2048, C=256, S=2)] * 2) == -1  # two states per lane
+    assert call([_desc(rans)] * 2) == -1  # 16 column tiles: split-K
+    assert call([a, b], ys=[0x3000, 0]) == -4  # a null y
+    bad = _desc(rans, rows=512, cols=2048)
+    bad.table_lds = None
+    assert call([a, bad]) == -4
+
+
 def test_product_fails_loudly_without_gpu(rans):
     import torch
     if torch.cuda.is_available():

@@ -73,7 +73,12 @@ struct WaveLayout {
     int wave_words;  // = raw_words
 };
 
-struct GemvArgs {
+// Per-matrix arguments of a GEMV launch.  A grouped launch runs up to
+// kMaxGroup matrices that share x (same cols, tile height, states per lane
+// and waves per workgroup) in one grid; matrix i owns the workgroups from
+// wg_begin[i] up to the next matrix's.
+constexpr int kMaxGroup = 4;
+struct MatArgs {
     const uint16_t* words;
     const uint32_t* tile_off;
     const uint8_t* slen;
@@ -83,17 +88,26 @@ struct GemvArgs {
     const int32_t* esc_pos;
     const int32_t* esc_val;
     const float* step;
-    const void* x;
     float* y;
-    float* partial;      // [ngroups][B][rows]
+    int rows, C, ncb;
+    int has_esc;    // 0: the side table is empty
+    int raw_words;  // LDS words of this matrix's staged block (largest block + 8)
+};
+
+struct GemvArgs {
+    // first workgroup of matrix i; INT_MAX for unused slots, so the matrix
+    // of a workgroup is the number of slots 1.. whose start it has reached
+    int wg_begin[kMaxGroup];
+    const void* x;
+    float* partial;      // [ngroups][B][rows] (one matrix only)
     uint32_t* counters;  // [rows/R]
-    int rows, cols, C, ncb, ngroups;
-    int W;        // waves per workgroup (= blockDim.x / 64, as a kernel argument)
-    int nb;       // x/y rows of this launch, 1..B: a batch-4 kernel also runs a
-                  // remainder of 2 or 3 (its other rows re-read the last x row
-                  // and store nothing)
-    int has_esc;  // 0: the side table is empty
-    WaveLayout L;
+    int cols, ngroups;
+    int W;           // waves per workgroup (= blockDim.x / 64, as a kernel argument)
+    int nb;          // x/y rows of this launch, 1..B: a batch-4 kernel also runs a
+                     // remainder of 2 or 3 (its other rows re-read the last x row
+                     // and store nothing)
+    int wave_words;  // per-wave LDS stride (the largest raw_words of the group)
+    MatArgs mat[kMaxGroup];
 };
 
 struct DecodeArgs {
@@ -388,7 +402,9 @@ __device__ __forceinline__ void lds_add(float* p, float v) {
 template <int R>
 constexpr bool kEscapesInLds = R >= 32;
 
-template <int R, int S, int B, bool XBF16, bool REFILL>
+// GROUP: a grouped launch (several matrices, slot found per workgroup);
+// otherwise slot 0 only, read at fixed kernel-argument offsets.
+template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs a) {
     __shared__ __align__(16) TabEntry tab[kProbM];
     __shared__ float red[kMaxWaves * R * B];
@@ -398,35 +414,45 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     const int W = a.W;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar tile math
     const int lane = threadIdx.x & 63;
-    uint16_t* raw = dyn + (size_t)wave * a.L.wave_words;
+    uint16_t* raw = dyn + (size_t)wave * a.wave_words;
 
-    const int rb = blockIdx.x / a.ngroups;
-    const int g = blockIdx.x - rb * a.ngroups;
-    const int cb = g * W + wave;  // W divides ncb: every wave has a tile
-    const int t = rb * a.ncb + cb;
+    // This workgroup's matrix.  A grouped launch reads its slot through an
+    // index (one more dependent scalar load); a single-matrix launch reads
+    // slot 0 at fixed offsets, fetched with the rest of the arguments.
+    int mi = 0;
+    if constexpr (GROUP) {
+#pragma unroll
+        for (int i = 1; i < kMaxGroup; i++) mi += (int)blockIdx.x >= a.wg_begin[i] ? 1 : 0;
+    }
+    const MatArgs& m = a.mat[GROUP ? mi : 0];
     // Every kernel argument the prologue needs, fetched in one scalar batch
     // (otherwise each is loaded, and waited for, at its first use).
-    asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.slen), "s"(a.table_lds),
-                 "s"(a.words), "s"(a.x), "s"(a.step), "s"(a.esc_tileptr), "s"(a.esc_pos),
-                 "s"(a.esc_val), "s"(a.C), "s"(a.cols),
-                 "s"(a.L.raw_words), "s"(a.W), "s"(a.ncb), "s"(a.ngroups), "s"(a.nb));
+    asm volatile("" ::"s"(m.tile_off), "s"(m.states), "s"(m.slen), "s"(m.table_lds),
+                 "s"(m.words), "s"(a.x), "s"(m.step), "s"(m.esc_tileptr), "s"(m.esc_pos),
+                 "s"(m.esc_val), "s"(m.C), "s"(a.cols),
+                 "s"(m.raw_words), "s"(a.W), "s"(m.ncb), "s"(a.ngroups), "s"(a.nb));
+    const int bid = (int)blockIdx.x - (GROUP ? a.wg_begin[mi] : 0);
+    const int rb = bid / a.ngroups;
+    const int g = bid - rb * a.ngroups;
+    const int cb = g * W + wave;  // W divides ncb: every wave has a tile
+    const int t = rb * m.ncb + cb;
 
     // Everything the wave needs from memory before decoding is requested in
     // one batch: initial states, stream offsets, the first block of x and
     // step, the table and the tile block.
-    const int nk = a.C / nst;
-    const int colbase = cb * a.C + lane;
+    const int nk = m.C / nst;
+    const int colbase = cb * m.C + lane;
     // The tile extent is loaded first: the block copy waits for it, and
     // loads complete in order, so nothing issued after it delays that copy.
-    const TileOff to = load_tile_off(a.tile_off, t);
+    const TileOff to = load_tile_off(m.tile_off, t);
     // This tile's range of the escape side table (lanes 0, 1), also needed early.
-    const int tp = a.esc_tileptr[t + min(lane, 1)];
+    const int tp = m.esc_tileptr[t + min(lane, 1)];
     asm volatile("" ::: "memory");  // keep these two loads first
     uint32_t st0[S], len0[S];
 #pragma unroll
     for (int s = 0; s < S; s++) {
-        st0[s] = a.states[t * nst + 64 * s + lane];
-        len0[s] = a.slen[t * nst + 64 * s + lane];
+        st0[s] = m.states[t * nst + 64 * s + lane];
+        len0[s] = m.slen[t * nst + 64 * s + lane];
     }
     // x and step for KU column steps are loaded one block ahead of use, so
     // their latency overlaps the decode of the current block.  They are
@@ -444,7 +470,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
             const_cast<uint8_t*>(static_cast<const uint8_t*>(a.x)) + (size_t)min(b, a.nb - 1) * a.cols * XS,
             0, a.cols * XS, kBufWord3);
     const __amdgpu_buffer_rsrc_t srs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.step), 0, a.cols * 4, kBufWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(m.step), 0, a.cols * 4, kBufWord3);
     // bf16 values kept as __bf16 (an integer register pin would be widened
     // first, at the cost of a mask per value), or f32 bits
     using XRaw = std::conditional_t<XBF16, __bf16, uint32_t>;
@@ -467,7 +493,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     };
     load_block(0);
     uint32_t o0, n16;
-    tile_extent(to, true, a.L.raw_words, o0, n16);
+    tile_extent(to, true, m.raw_words, o0, n16);
     // Each wave adds its own tile's escapes, in chunks of 64 side-table
     // entries.  They run in column order within the tile, so a chunk's x and
     // step gathers fall in a narrow column range (a few cache lines).  The
@@ -476,25 +502,25 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     // costs nothing more), and their x and step gathers go out before the
     // decode loop, their values kept raw until after the loop, so that
     // latency overlaps the decode.
-    const bool esc = a.has_esc;  // kernel-uniform
+    const bool esc = m.has_esc;  // kernel-uniform
     const int e_lo = esc ? __builtin_amdgcn_readlane(tp, 0) : 0;
     const int e_hi = esc ? __builtin_amdgcn_readlane(tp, 1) : 0;
     asm volatile("" ::"s"(e_lo), "s"(e_hi));
-    stage_tile(raw, a.words, o0, n16, lane);
-    stage_table(tab, a.table_lds, wave, W, lane);
+    stage_tile(raw, m.words, o0, n16, lane);
+    stage_table(tab, m.table_lds, wave, W, lane);
     constexpr int P = 2;  // chunks per wave prefetched: 128 escapes per tile
-    const int cbase = cb * a.C;
+    const int cbase = cb * m.C;
     // tile column of an entry, clamped into the tile so that no side-table
     // content can send a gather outside x or step
-    auto esc_col = [&](int pos) { return cbase + (int)min((uint32_t)pos >> 8, (uint32_t)(a.C - 1)); };
+    auto esc_col = [&](int pos) { return cbase + (int)min((uint32_t)pos >> 8, (uint32_t)(m.C - 1)); };
     int epos[P], eval[P];
 #pragma unroll
     for (int p = 0; p < P; p++) {
         epos[p] = eval[p] = 0;
         if (e_lo + 64 * p < e_hi) {  // wave-uniform
             const int ec = min(e_lo + 64 * p + lane, e_hi - 1);
-            epos[p] = a.esc_pos[ec];
-            eval[p] = a.esc_val[ec];
+            epos[p] = m.esc_pos[ec];
+            eval[p] = m.esc_val[ec];
         }
     }
     wait_vm();
@@ -536,7 +562,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         for (int p = 0; p < P; p++) {
             asm volatile("" : "+v"(epos[p]), "+v"(eval[p]));
             const int col = esc_col(epos[p]);
-            esr[p] = __float_as_uint(a.step[col]);
+            esr[p] = __float_as_uint(m.step[col]);
 #pragma unroll
             for (int b = 0; b < B; b++)
                 exr[p][b] = load_x_bits(a.x, (int64_t)min(b, a.nb - 1) * a.cols + col, XBF16);
@@ -601,9 +627,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         for (int e0 = e_lo + 64 * P; e0 < e_hi; e0 += 64) {
             const int e = e0 + lane;
             const int ec = min(e, e_hi - 1);
-            const int pos = a.esc_pos[ec];
+            const int pos = m.esc_pos[ec];
             const int col = esc_col(pos);
-            const float ve = e < e_hi ? (float)a.esc_val[ec] * a.step[col] : 0.f;
+            const float ve = e < e_hi ? (float)m.esc_val[ec] * m.step[col] : 0.f;
 #pragma unroll
             for (int b = 0; b < B; b++)
                 ev[b] = ve * load_x(a.x, (int64_t)min(b, a.nb - 1) * a.cols + col, XBF16);
@@ -658,10 +684,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         for (int e0 = e_lo + 64 * P; e0 < e_hi; e0 += 64) {
             const int e = e0 + lane;
             const int ec = min(e, e_hi - 1);
-            const int pos = a.esc_pos[ec];
+            const int pos = m.esc_pos[ec];
             const int re = pos & 0xFF;
             const int col = esc_col(pos);
-            const float ve = (float)a.esc_val[ec] * a.step[col];
+            const float ve = (float)m.esc_val[ec] * m.step[col];
             float xb[B];
 #pragma unroll
             for (int b = 0; b < B; b++)
@@ -686,7 +712,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     if (a.ngroups == 1) {
         for (int i = tid; i < NRB; i += nthr) {
             const int r = i / B, b = i - r * B;
-            if (b < a.nb) a.y[(int64_t)b * a.rows + rb * R + r] = total(i);
+            if (b < a.nb) m.y[(int64_t)b * m.rows + rb * R + r] = total(i);
         }
         return;
     }
@@ -701,7 +727,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     // back or invalidate the whole L2 of the XCD.
     for (int i = tid; i < NRB; i += nthr) {
         const int r = i / B, b = i - r * B;
-        __hip_atomic_store(&a.partial[((int64_t)g * B + b) * a.rows + rb * R + r], total(i),
+        __hip_atomic_store(&a.partial[((int64_t)g * B + b) * m.rows + rb * R + r], total(i),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -717,9 +743,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
             const int r = i / B, b = i - r * B;
             float s = 0.f;
             for (int gg = 0; gg < a.ngroups; gg++)
-                s += __hip_atomic_load(&a.partial[((int64_t)gg * B + b) * a.rows + rb * R + r],
+                s += __hip_atomic_load(&a.partial[((int64_t)gg * B + b) * m.rows + rb * R + r],
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (b < a.nb) a.y[(int64_t)b * a.rows + rb * R + r] = s;
+            if (b < a.nb) m.y[(int64_t)b * m.rows + rb * R + r] = s;
         }
         if (tid == 0)
             __hip_atomic_store(&a.counters[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -959,25 +985,37 @@ hipError_t ensure_lds(const void* fn, size_t bytes, int static_bytes) {
     return e;
 }
 
-template <int R, int S, int B, bool XBF16, bool REFILL>
+template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP>
 int launch_gemv_t(const GemvArgs& a, int waves, size_t lds, int grid, hipStream_t stream) {
-    const void* fn = reinterpret_cast<const void*>(&rans_w64_gemv_kernel<R, S, B, XBF16, REFILL>);
+    const void* fn =
+        reinterpret_cast<const void*>(&rans_w64_gemv_kernel<R, S, B, XBF16, REFILL, GROUP>);
     hipError_t e = ensure_lds(fn, lds, gemv_static_lds(R));
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((rans_w64_gemv_kernel<R, S, B, XBF16, REFILL>), dim3(grid), dim3(64 * waves),
+    hipLaunchKernelGGL((rans_w64_gemv_kernel<R, S, B, XBF16, REFILL, GROUP>), dim3(grid),
+                       dim3(64 * waves),
                        lds, stream, a);
     return (int)hipGetLastError();
 }
 
-// var: bit 0 = bf16 x, bit 1 = refill-only word fetch.
+// var: bit 0 = bf16 x, bit 1 = refill-only word fetch, bit 2 = grouped
+// launch (compiled for one state per lane only).
+template <int R, int S, int B, bool GROUP>
+int dispatch_xf(const GemvArgs& a, int var, int waves, size_t lds, int grid, hipStream_t st) {
+    switch (var & 3) {
+        case 0: return launch_gemv_t<R, S, B, false, false, GROUP>(a, waves, lds, grid, st);
+        case 1: return launch_gemv_t<R, S, B, true, false, GROUP>(a, waves, lds, grid, st);
+        case 2: return launch_gemv_t<R, S, B, false, true, GROUP>(a, waves, lds, grid, st);
+        default: return launch_gemv_t<R, S, B, true, true, GROUP>(a, waves, lds, grid, st);
+    }
+}
+
 template <int R, int S, int B>
 int dispatch_v(const GemvArgs& a, int var, int waves, size_t lds, int grid, hipStream_t st) {
-    switch (var) {
-        case 0: return launch_gemv_t<R, S, B, false, false>(a, waves, lds, grid, st);
-        case 1: return launch_gemv_t<R, S, B, true, false>(a, waves, lds, grid, st);
-        case 2: return launch_gemv_t<R, S, B, false, true>(a, waves, lds, grid, st);
-        default: return launch_gemv_t<R, S, B, true, true>(a, waves, lds, grid, st);
+    if (var & 4) {
+        if constexpr (S == 1) return dispatch_xf<R, S, B, true>(a, var, waves, lds, grid, st);
+        return RANS_EUNSUPPORTED;
     }
+    return dispatch_xf<R, S, B, false>(a, var, waves, lds, grid, st);
 }
 
 template <int R, int S>
@@ -1087,48 +1125,59 @@ extern "C" int64_t rans_gemv_workspace_bytes(const rans_w64_matrix* m, int batch
     return (int64_t)counters_bytes(m) + (int64_t)ngroups * bmax * m->rows * 4;
 }
 
-extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
-                                void* y, hipStream_t stream) {
-    if (!valid_geometry(m)) return RANS_EGEOMETRY;
-    if (!valid_pointers(m) || !x || !y || batch <= 0) return RANS_EARG;
-    if (x_dtype != RANS_X_F32 && x_dtype != RANS_X_BF16) return RANS_EARG;
-    if (!supported_rs(m->R, m->S)) return RANS_EUNSUPPORTED;
-    const int waves = gemv_waves(m);
+namespace {
+
+// One launch over n matrices that share x (n = 1: any single matrix,
+// split-K included; n > 1: a group, validated by the caller).
+int launch_gemv_common(const rans_w64_matrix* const* ms, int n, const void* x, int x_dtype,
+                       int batch, float* const* ys, hipStream_t stream) {
+    const rans_w64_matrix* m0 = ms[0];
+    const int waves = gemv_waves(m0);
     if (!waves) return RANS_EGEOMETRY;
-    const int ncb = m->cols / m->C;
-    const int ngroups = ncb / waves;
-    if (ngroups > 1 && (!m->workspace || m->workspace_bytes < rans_gemv_workspace_bytes(m, batch)))
+    const int ncb0 = m0->cols / m0->C;
+    const int ngroups = ncb0 / waves;
+    if (ngroups > 1 &&
+        (!m0->workspace || m0->workspace_bytes < rans_gemv_workspace_bytes(m0, batch)))
         return RANS_EWORKSPACE;
     const bool xbf16 = x_dtype == RANS_X_BF16;
     const size_t xsz = xbf16 ? 2 : 4;
-    const int fetch = m->flags & RANS_F_WORDS_MASK;
-    const bool refill = fetch == RANS_F_WORDS_REFILL || (fetch == 0 && m->R >= 3);
-    const int var = (xbf16 ? 1 : 0) | (refill ? 2 : 0);
+    const int fetch = m0->flags & RANS_F_WORDS_MASK;
+    const bool refill = fetch == RANS_F_WORDS_REFILL || (fetch == 0 && m0->R >= 3);
+    const int var = (xbf16 ? 1 : 0) | (refill ? 2 : 0) | (n > 1 ? 4 : 0);
 
-    GemvArgs a;
-    a.words = m->words;
-    a.tile_off = m->tile_off;
-    a.slen = m->slen;
-    a.states = m->states;
-    a.table_lds = reinterpret_cast<const uint4*>(m->table_lds);
-    a.esc_tileptr = m->esc_tileptr;
-    a.esc_pos = m->esc_pos;
-    a.esc_val = m->esc_val;
-    a.step = m->step;
-    a.rows = m->rows;
-    a.cols = m->cols;
-    a.C = m->C;
-    a.ncb = ncb;
+    GemvArgs a = {};
+    for (int i = 0; i < kMaxGroup; i++) a.wg_begin[i] = INT32_MAX;
+    a.cols = m0->cols;
     a.ngroups = ngroups;
     a.W = waves;
-    a.has_esc = !(m->flags & RANS_F_NO_ESCAPES);
-    a.L = wave_layout(m);
-    a.counters = ngroups > 1 ? static_cast<uint32_t*>(m->workspace) : nullptr;
-    a.partial = ngroups > 1
-                    ? reinterpret_cast<float*>(static_cast<uint8_t*>(m->workspace) + counters_bytes(m))
-                    : nullptr;
-    const size_t lds = lds_bytes(waves, a.L);
-    const int grid = (m->rows / m->R) * ngroups;
+    a.counters = ngroups > 1 ? static_cast<uint32_t*>(m0->workspace) : nullptr;
+    a.partial = ngroups > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(m0->workspace) +
+                                                       counters_bytes(m0))
+                            : nullptr;
+    int grid = 0;
+    a.wave_words = 0;
+    for (int i = 0; i < n; i++) {
+        const rans_w64_matrix* m = ms[i];
+        MatArgs& d = a.mat[i];
+        d.words = m->words;
+        d.tile_off = m->tile_off;
+        d.slen = m->slen;
+        d.states = m->states;
+        d.table_lds = reinterpret_cast<const uint4*>(m->table_lds);
+        d.esc_tileptr = m->esc_tileptr;
+        d.esc_pos = m->esc_pos;
+        d.esc_val = m->esc_val;
+        d.step = m->step;
+        d.rows = m->rows;
+        d.C = m->C;
+        d.ncb = m->cols / m->C;
+        d.has_esc = !(m->flags & RANS_F_NO_ESCAPES);
+        d.raw_words = wave_layout(m).raw_words;
+        a.wg_begin[i] = grid;
+        grid += (m->rows / m->R) * ngroups;
+        if (d.raw_words > a.wave_words) a.wave_words = d.raw_words;
+    }
+    const size_t lds = (size_t)waves * a.wave_words * 2;
 
     // Batches run in chunks of up to 4 vectors on the batch-4 kernel, a
     // single remaining vector on the batch-1 kernel.
@@ -1136,14 +1185,58 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
     while (done < batch) {
         const int nb = batch - done >= 4 ? 4 : batch - done;
         const int B = nb >= 2 ? 4 : 1;
-        a.x = static_cast<const uint8_t*>(x) + (size_t)done * m->cols * xsz;
-        a.y = static_cast<float*>(y) + (size_t)done * m->rows;
+        a.x = static_cast<const uint8_t*>(x) + (size_t)done * m0->cols * xsz;
+        for (int i = 0; i < n; i++) a.mat[i].y = ys[i] + (size_t)done * ms[i]->rows;
         a.nb = nb;
-        const int rc = dispatch_gemv(a, m->R, m->S, B, var, waves, lds, grid, stream);
+        const int rc = dispatch_gemv(a, m0->R, m0->S, B, var, waves, lds, grid, stream);
         if (rc != 0) return rc;
         done += nb;
     }
     return 0;
+}
+
+bool check_gemv_args(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
+                     const void* y, int& rc) {
+    if (!valid_geometry(m)) return rc = RANS_EGEOMETRY, false;
+    if (!valid_pointers(m) || !x || !y || batch <= 0) return rc = RANS_EARG, false;
+    if (x_dtype != RANS_X_F32 && x_dtype != RANS_X_BF16) return rc = RANS_EARG, false;
+    if (!supported_rs(m->R, m->S)) return rc = RANS_EUNSUPPORTED, false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
+                                void* y, hipStream_t stream) {
+    int rc = 0;
+    if (!check_gemv_args(m, x, x_dtype, batch, y, rc)) return rc;
+    float* ys[1] = {static_cast<float*>(y)};
+    return launch_gemv_common(&m, 1, x, x_dtype, batch, ys, stream);
+}
+
+extern "C" int launch_rans_gemv_group(const rans_w64_matrix* const* ms, int n, const void* x,
+                                      int x_dtype, int batch, float* const* ys,
+                                      hipStream_t stream) {
+    if (!ms || !ys || n <= 0) return RANS_EARG;
+    if (n > kMaxGroup) return RANS_EUNSUPPORTED;
+    int rc = 0;
+    for (int i = 0; i < n; i++)
+        if (!check_gemv_args(ms[i], x, x_dtype, batch, ys[i], rc)) return rc;
+    const rans_w64_matrix* m0 = ms[0];
+    if (m0->S != 1) return RANS_EUNSUPPORTED;
+    const int waves = gemv_waves(m0);
+    if (!waves) return RANS_EGEOMETRY;
+    for (int i = 0; i < n; i++) {
+        const rans_w64_matrix* m = ms[i];
+        if (m->cols != m0->cols || m->R != m0->R || m->S != m0->S) return RANS_EUNSUPPORTED;
+        const int w = gemv_waves(m);
+        // one workgroup per tile row (no split-K), the same waves per workgroup
+        if (w != waves || (m->cols / m->C) != w) return RANS_EUNSUPPORTED;
+        // the group's LDS stride is its largest block region
+        if (lds_bytes(waves, wave_layout(m)) + gemv_static_lds(m->R) > (size_t)kLdsMax)
+            return RANS_EGEOMETRY;
+    }
+    return launch_gemv_common(ms, n, x, x_dtype, batch, ys, stream);
 }
 
 extern "C" int launch_rans_decode(const rans_w64_matrix* m, void* out_bf16, hipStream_t stream) {

@@ -61,7 +61,8 @@ class RansMatrixDesc(ctypes.Structure):
                 ("workspace_bytes", ctypes.c_int64)]
 
 
-EXPORTS = ("launch_rans_gemv", "rans_gemv_workspace_bytes", "launch_rans_decode",
+EXPORTS = ("launch_rans_gemv", "rans_gemv_workspace_bytes", "launch_rans_gemv_group",
+           "launch_rans_decode",
            "launch_rans_decode_codes", "launch_int4_gemv", "rans_build_table", "rans_table_lds",
            "rans_w64_encode", "rans_w64_encode_fetch", "rans_w64_encode_free",
            "rans_w64_decode_host")
@@ -92,6 +93,8 @@ def load_lib(path=LIB):
     sig = {
         "launch_rans_gemv": ([D, P, ctypes.c_int, ctypes.c_int, P, P], ctypes.c_int),
         "rans_gemv_workspace_bytes": ([D, ctypes.c_int], I64),
+        "launch_rans_gemv_group": ([P, ctypes.c_int, P, ctypes.c_int, ctypes.c_int, P, P],
+                                   ctypes.c_int),
         "launch_rans_decode": ([D, P, P], ctypes.c_int),
         "launch_rans_decode_codes": ([D, P, P], ctypes.c_int),
         "launch_int4_gemv": ([P, P, P, ctypes.c_int, ctypes.c_int, P], ctypes.c_int),
@@ -223,7 +226,7 @@ def encode(codes, R, C, S=1, threads=None):
                 entropy_model=float(-np.log2(p).mean()))
 
 
-def pick_tiling(rows, cols, R=None, S=1, target_states=None):
+def pick_tiling(rows, cols, R=None, S=1, target_states=None, max_ncb=None):
     """A legal (R, C) for the w64 format: C a multiple of 64*S dividing cols,
     R in {1, 2, 3, 4, 8, 16}, or 35 at S=1 (rows of 8960 = 256 x 35: 8960 x
     1536 becomes 2048 tiles of 35 x 192, two waves on every SIMD).  Chosen by
@@ -242,11 +245,18 @@ def pick_tiling(rows, cols, R=None, S=1, target_states=None):
     - column tiles per tile row (ncb): 8 is best (8 waves of a workgroup
       share one LDS table, so more waves fit per CU), then 4-7 and 16 (the
       latter needs the split-K reduction); fewer than 4 repeat the table
-      staging more often per tile."""
+      staging more often per tile.
+
+    R: one tile height, or a list of candidates (default: every compiled
+    one dividing rows); max_ncb: at most this many column tiles."""
     nst = 64 * S
-    cands = [c for c in range(nst, cols + 1, nst) if cols % c == 0]
+    cands = [c for c in range(nst, cols + 1, nst)
+             if cols % c == 0 and (max_ncb is None or cols // c <= max_ncb)]
     assert cands, f"cols={cols} has no divisor that is a multiple of {nst}"
-    Rs = [R] if R else [r for r in (SUPPORTED_R if S == 1 else SUPPORTED_R[1:]) if rows % r == 0]
+    if R is None:
+        Rs = [r for r in (SUPPORTED_R if S == 1 else SUPPORTED_R[1:]) if rows % r == 0]
+    else:
+        Rs = [R] if isinstance(R, int) else list(R)
     n = rows * cols
     if target_states:
         target = target_states
@@ -454,6 +464,58 @@ class RansMatrix:
                                                torch.cuda.current_stream().cuda_stream)
         assert rc == 0, f"HIP error {rc}"
         return out
+
+
+GROUP_MAX = 4
+_EUNSUPPORTED, _EGEOMETRY = -1, -2
+
+
+def pick_group_tiling(rows_list, cols, S=1):
+    """One (R, C) for matrices that share x (a layer's q, k, v or gate, up),
+    so that gemv_group can run them in one launch: the tiling pick_tiling
+    gives the stacked matrix, among tile heights that divide every member's
+    rows, with at most 8 column tiles (one workgroup per tile row)."""
+    Rs = [r for r in (SUPPORTED_R if S == 1 else SUPPORTED_R[1:])
+          if all(n % r == 0 for n in rows_list)]
+    assert Rs, f"no compiled tile height divides all of {list(rows_list)}"
+    return pick_tiling(sum(rows_list), cols, R=Rs, S=S, max_ncb=8)
+
+
+def gemv_group(matrices, x, ys=None):
+    """[m.gemv(x) for m in matrices] for up to 4 RansMatrix objects sharing
+    x, in one launch (launch_rans_gemv_group) when they can share one: same
+    cols and R, one state per lane, one workgroup per tile row (encode them
+    with pick_group_tiling).  Otherwise one launch per matrix.  Results are
+    bitwise those of separate gemv calls.  Returns the list of y."""
+    ms = list(matrices)
+    assert 0 < len(ms), "no matrices"
+    assert x.is_cuda, "x must be a device tensor"
+    squeeze = x.dim() == 1
+    xb = x.reshape(1, -1) if squeeze else x
+    if xb.dtype == torch.bfloat16:
+        xd = X_BF16
+    else:
+        xb, xd = xb.float(), X_F32
+    xb = xb.contiguous()
+    B = xb.shape[0]
+    if ys is None:
+        ys = [torch.empty((B, m.rows) if not squeeze else (m.rows,), device="cuda",
+                          dtype=torch.float32) for m in ms]
+    assert len(ys) == len(ms)
+    for m, y in zip(ms, ys):
+        assert xb.shape[-1] == m.cols
+        assert y.dtype == torch.float32 and y.is_contiguous() and y.numel() == B * m.rows
+    if 1 < len(ms) <= GROUP_MAX:
+        descs = (ctypes.c_void_p * len(ms))(*[ctypes.addressof(m._desc) for m in ms])
+        yps = (ctypes.c_void_p * len(ms))(*[y.data_ptr() for y in ys])
+        rc = ms[0].lib.launch_rans_gemv_group(descs, len(ms), xb.data_ptr(), xd, B, yps,
+                                              torch.cuda.current_stream().cuda_stream)
+        if rc == 0:
+            return ys
+        assert rc in (_EUNSUPPORTED, _EGEOMETRY), f"HIP error {rc}"
+    for m, y in zip(ms, ys):
+        m.gemv(xb if not squeeze else xb[0], y)
+    return ys
 
 
 class Int4Matrix:

@@ -21,7 +21,7 @@ import torch
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 import rans  # noqa: E402
-from rans import encode, pick_tiling  # noqa: E402,F401
+from rans import encode, gemv_group, pick_group_tiling, pick_tiling  # noqa: E402,F401
 
 RES = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "results")
 
@@ -296,11 +296,20 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
     return out
 
 
-def chain(bits=3.25, layers=28, seed=0, iters=3):
+# projections of a layer that read the same activations
+CHAIN_GROUPS = {"q": "qkv", "k": "qkv", "v": "qkv", "gate": "mlp", "up": "mlp"}
+
+
+def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False):
     """Per-token chain of 7*layers batch-1 GEMVs over a random-init
     Qwen2.5-1.5B-shaped weight set (one table per matrix, ECSQ-like Laplace
     codes at `bits` bits/weight), graph-captured and replayed; the same chain
-    with bf16 F.linear.  Returns the total weight-pass latency of both."""
+    with bf16 F.linear.  Returns the total weight-pass latency of both.
+
+    grouped: q, k, v and gate, up of a layer each run as one grouped launch
+    (gemv_group, tiled with pick_group_tiling); the bf16 chain then runs q, k,
+    v as one F.linear over the concatenated weights (faster than three),
+    gate and up separately (the concatenated shape is slower in rocBLAS)."""
     lib = rans.build()
     rng = np.random.default_rng(seed)
     mats, Ws, xs = [], [], {}
@@ -309,7 +318,16 @@ def chain(bits=3.25, layers=28, seed=0, iters=3):
     # one step per shape, chosen on a sample, so every layer has ~`bits` bits
     deltas = {}
     fetch = {}
-    for name, rows, cols in qwen15b_layer_shapes():
+    shapes = qwen15b_layer_shapes()
+    tiling = {name: chain_tiling(rows, cols) for name, rows, cols in shapes}
+    if grouped:
+        for g in set(CHAIN_GROUPS.values()):
+            members = [(n, r, c) for n, r, c in shapes if CHAIN_GROUPS.get(n) == g]
+            t = pick_group_tiling([r for _, r, _ in members], members[0][2])
+            for n, _, _ in members:
+                tiling[n] = t
+    steps = []  # launches in chain order: lists of (name, matrix)
+    for name, rows, cols in shapes:
         sample = rng.laplace(size=1 << 20)
         lo, hi = -12.0, 6.0
         for _ in range(40):
@@ -318,16 +336,22 @@ def chain(bits=3.25, layers=28, seed=0, iters=3):
             lo, hi = (mid, hi) if h > bits else (lo, mid)
         deltas[name] = np.exp((lo + hi) / 2)
     for layer in range(layers):
-        for name, rows, cols in qwen15b_layer_shapes():
+        for name, rows, cols in shapes:
             codes = np.round(rng.laplace(size=(rows, cols)) / deltas[name]).astype(np.int32)
             step = torch.from_numpy(lognormal_steps(cols, seed=seed + layer))
-            R, C = chain_tiling(rows, cols)
+            R, C = tiling[name]
             enc = encode(codes, R, C, 1)
             # word-fetch policy tuned once per shape, on the first layer
             m = rans.RansMatrix(enc, step, lib, flags=fetch.get(name, 0))
             if name not in fetch:
                 fetch[name] = m.tune()
             mats.append(m)
+            g = CHAIN_GROUPS.get(name) if grouped else None
+            if g and steps and CHAIN_GROUPS.get(steps[-1][0][0]) == g \
+                    and len(steps[-1]) < rans.GROUP_MAX:
+                steps[-1].append((name, m))
+            else:
+                steps.append([(name, m)])
             nbytes += m.nbytes
             nweights += codes.size
             Ws.append((torch.from_numpy(codes.astype(np.float32)) * step).bfloat16().cuda())
@@ -335,11 +359,25 @@ def chain(bits=3.25, layers=28, seed=0, iters=3):
                 xs[cols] = torch.randn(cols, device="cuda").bfloat16()
             print(f"chain: layer {layer} {name} encoded", file=sys.stderr, flush=True) \
                 if name == "down" and layer % 7 == 0 else None
-    ys = {r: torch.empty(r, device="cuda") for r in {m.rows for m in mats}}
+    ys = {n: torch.empty(r, device="cuda") for n, r, _ in shapes}
+    if grouped:  # q, k, v weights of a layer concatenated for the bf16 chain
+        Wl, i = [], 0
+        for step_ in steps:
+            ws = Ws[i:i + len(step_)]
+            i += len(step_)
+            if CHAIN_GROUPS.get(step_[0][0]) == "qkv":
+                Wl.append(torch.cat(ws, 0).contiguous())
+            else:
+                Wl.extend(ws)
+        Ws = Wl
 
     def run_rans():
-        for m in mats:
-            m.gemv(xs[m.cols], ys[m.rows])
+        for step_ in steps:
+            if len(step_) > 1:
+                gemv_group([m for _, m in step_], xs[step_[0][1].cols], [ys[n] for n, _ in step_])
+            else:
+                n, m = step_[0]
+                m.gemv(xs[m.cols], ys[n])
 
     def run_bf16():
         for W in Ws:
@@ -347,8 +385,9 @@ def chain(bits=3.25, layers=28, seed=0, iters=3):
 
     t_rans = timeit_graph(run_rans, iters, warmup=2)
     t_bf16 = timeit_graph(run_bf16, iters, warmup=2)
-    return dict(config="Qwen2.5-1.5B-shaped weight set, 28 layers x 7 matrices, batch 1",
-                gemvs=len(mats), weights=nweights, bits_target=bits,
+    return dict(config="Qwen2.5-1.5B-shaped weight set, 28 layers x 7 matrices, batch 1"
+                + (", q/k/v and gate/up grouped" if grouped else ""),
+                gemvs=len(mats), launches=len(steps), weights=nweights, bits_target=bits,
                 bits_total=8 * nbytes / nweights, compressed_MB=nbytes / 1e6,
                 bf16_MB=nweights * 2 / 1e6, t_rans_us=t_rans, t_bf16_us=t_bf16,
                 effective_GBps=nweights * 2 / t_rans / 1e3, speedup_vs_bf16=t_bf16 / t_rans)
@@ -358,7 +397,8 @@ def configs():
     """The benchmark configurations beyond the headline shape: MLP shapes at
     2.25 bits with 0.1% escapes, q_proj at 4.25 bits, the 27B-class shapes
     with Student-t codes and 1% escapes at batch 1 and 4, and the per-token
-    196-GEMV chain.  Prints one JSON line per result."""
+    196-GEMV chain with separate and with grouped launches.  Prints one JSON
+    line per result."""
     lib = rans.build()
     cases = [
         ("q_proj 4.25b gauss", 1536, 1536, 4.25, "gauss", 0.0, 1),
@@ -374,9 +414,10 @@ def configs():
         r["case"] = name
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}),
               flush=True)
-    r = chain()
-    print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}),
-          flush=True)
+    for grouped in (False, True):
+        r = chain(grouped=grouped)
+        print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}),
+              flush=True)
 
 
 def profile(rows=25600, cols=5120, bits=2.25, dist="student3", escape_frac=0.01, R=16, C=640,
