@@ -52,6 +52,11 @@ def test_tiny_qwen2_with_rans_linears(rans, lib):
     coded = copy.deepcopy(dense)
     names = L.replace_linears(coded, bits=6.0, lib=lib, tune=False)
     assert len(names) == 2 * 7  # q, k, v, o, gate, up, down per layer; lm_head stays dense
+    for layer in coded.model.layers:  # q/k/v and gate/up linked into grouped launches
+        att, mlp = layer.self_attn, layer.mlp
+        assert att.q_proj.group is att.k_proj.group is att.v_proj.group is not None
+        assert mlp.gate_proj.group is mlp.up_proj.group is not None
+        assert att.o_proj.group is None and mlp.down_proj.group is None
     # the dense twin gets exactly the dequantised weights code*step (fp32)
     for n in names:
         m = coded.get_submodule(n).matrix
@@ -67,6 +72,15 @@ def test_tiny_qwen2_with_rans_linears(rans, lib):
         # a longer prompt takes the prefill path (bf16-decoded weights + dense GEMM)
         long_ids = torch.randint(0, 512, (1, 12), generator=torch.Generator().manual_seed(2)).cuda()
         assert _rel(coded(long_ids).logits, dense(long_ids).logits) <= 2e-2
+        # one decode step: two grouped launches per layer (q/k/v, gate/up)
+        calls = []
+        real = rans.gemv_group
+        rans.gemv_group = lambda *a, **k: (calls.append(1), real(*a, **k))[1]
+        try:
+            coded(ids[:, :1])
+        finally:
+            rans.gemv_group = real
+        assert len(calls) == 2 * len(coded.model.layers)
         # greedy token loop with the KV cache: same tokens from both models
         out_d, out_c = dense(ids, use_cache=True), coded(ids, use_cache=True)
         pd, pc = out_d.past_key_values, out_c.past_key_values
@@ -79,3 +93,42 @@ def test_tiny_qwen2_with_rans_linears(rans, lib):
             out_c = coded(tc, past_key_values=pc, use_cache=True)
             pd, pc = out_d.past_key_values, out_c.past_key_values
             assert _rel(out_c.logits, out_d.logits) <= 1e-3
+
+
+def test_linear_group_reuses_one_launch(rans, lib):
+    """q, k, v RansLinears linked into a LinearGroup: the three calls with
+    one input make one grouped launch, and each output is bitwise that
+    module's own GEMV (plus bias).  A second call with the same input, an
+    in-place write to it, or another input launch again."""
+    import rans_linear as L
+    print("case LinearGroup q/k/v 1536+256+256 x 1536", flush=True)
+    g = torch.Generator().manual_seed(5)
+    R, C = rans.pick_group_tiling([1536, 256, 256], 1536)
+    mods = []
+    for rows in (1536, 256, 256):
+        codes, step = L.quantize_uniform(torch.randn(rows, 1536, generator=g) * 0.02, 3.5)
+        mods.append(L.RansLinear.from_codes(codes, step, torch.randn(rows, generator=g), lib,
+                                            tiling=(R, C, 1), tune=False))
+    group = L.LinearGroup(mods)
+    for m in mods:
+        m.group = group
+    calls = []
+    real = rans.gemv_group
+    rans.gemv_group = lambda *a, **k: (calls.append(1), real(*a, **k))[1]
+    try:
+        x = torch.randn(1, 2, 1536, generator=g).bfloat16().cuda()
+        ys = [m(x) for m in mods]
+        assert len(calls) == 1
+        xd = x.reshape(-1, 1536)
+        for m, y in zip(mods, ys):
+            want = (m.matrix.gemv(xd) + m.bias).to(torch.bfloat16).reshape(1, 2, -1)
+            assert torch.equal(y, want)
+        mods[1](x)               # k again with the same input: its result was taken
+        assert len(calls) == 2
+        x.mul_(1.0)              # an in-place write: the kept results are stale
+        mods[2](x)
+        assert len(calls) == 3
+        mods[0](x.clone())       # another tensor
+        assert len(calls) == 4
+    finally:
+        rans.gemv_group = real

@@ -7,11 +7,18 @@ batches (prefill), decodes the weight to bf16 once and calls the dense GEMM,
 which is then the faster path.  Inference only: the weight is not a
 parameter.
 
+Projections that read the same activations (a decoder layer's q, k, v, or
+its gate and up) can be linked into a LinearGroup: the first member called
+computes all members' products in one grouped launch, and the others return
+theirs when called with the same input.  replace_linears links them by name.
+
 quantize_uniform is a plain uniform quantiser (one step per tensor, chosen
 for a target code entropy) so that ordinary nn.Linear layers can be
 converted in tests and demos; the reference's ECSQ-GPTQ quantiser
 (exp/quant.py) is outside this repository.
 """
+import weakref
+
 import numpy as np
 import torch
 
@@ -50,12 +57,42 @@ def quantize_uniform(weight, bits, iters=40, sample=1 << 22, seed=0):
     return codes, np.full(w.shape[1], delta, np.float32)
 
 
+class LinearGroup:
+    """RansLinear modules that read the same input: a decoder layer's q, k
+    and v projections, or its gate and up.  When a member is called (with a
+    decode-sized input), every member's product is computed in one grouped
+    launch (rans.gemv_group); the other members' results are kept and
+    returned when those members are called with the same input tensor,
+    unmodified, so Hugging Face's q_proj(h), k_proj(h), v_proj(h) costs one
+    launch.  A member called with any other input computes afresh.  The
+    members need the same tiling (rans.pick_group_tiling)."""
+
+    def __init__(self, members):
+        self.members = list(members)
+        self._x = None        # weak reference to the input of the last launch
+        self._version = None  # its version counter then (in-place writes bump it)
+        self._pending = {}    # member index -> its product, not yet returned
+
+    def product(self, member, x, xd):
+        """member's x @ W^T (no bias) for the module input x, flattened and
+        converted to xd (rows x in_features, f32 or bf16)."""
+        i = next(j for j, m in enumerate(self.members) if m is member)
+        if (self._x is not None and self._x() is x and self._version == x._version
+                and i in self._pending):
+            return self._pending.pop(i)
+        ys = rans.gemv_group([m.matrix for m in self.members], xd)
+        self._x, self._version = weakref.ref(x), x._version
+        self._pending = {j: y for j, y in enumerate(ys) if j != i}
+        return ys[i]
+
+
 class RansLinear(torch.nn.Module):
     """y = x @ W^T + b with W = code * step held as a rans.RansMatrix."""
 
     def __init__(self, matrix, bias=None):
         super().__init__()
         self.matrix = matrix
+        self.group = None  # a LinearGroup this module belongs to, if any
         self.in_features = matrix.cols
         self.out_features = matrix.rows
         if bias is not None:
@@ -98,6 +135,8 @@ class RansLinear(torch.nn.Module):
         if xd.shape[0] > PREFILL_ROWS:
             w = self.matrix.decode()  # bf16 code*step, then the dense GEMM
             y = torch.nn.functional.linear(xd.to(torch.bfloat16), w).float()
+        elif self.group is not None:
+            y = self.group.product(self, x, xd.contiguous())
         else:
             y = self.matrix.gemv(xd.contiguous())
         if self.bias is not None:
@@ -110,23 +149,56 @@ class RansLinear(torch.nn.Module):
         m = self.matrix
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
                 f"bias={self.bias is not None}, tiles={m.R}x{m.C}x{m.S}, "
-                f"bits_per_weight={8 * m.nbytes / (m.rows * m.cols):.3f}")
+                f"bits_per_weight={8 * m.nbytes / (m.rows * m.cols):.3f}, "
+                f"grouped={self.group is not None}")
 
 
-def replace_linears(module, bits=3.25, lib=None, skip=("lm_head",), tune=True):
+# sibling projections that read the same activations (Hugging Face names)
+GROUPS = (("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj"))
+
+
+def replace_linears(module, bits=3.25, lib=None, skip=("lm_head",), tune=True, groups=GROUPS):
     """Swap every nn.Linear of `module` (except names containing an entry of
     `skip`) for a RansLinear quantised at `bits`.  Returns the names swapped.
     Layers whose in_features is not a multiple of 64 (the w64 tile width)
-    are left dense."""
+    are left dense.  Siblings named in one entry of `groups` (same parent,
+    same in_features) are encoded with one tiling and linked into a
+    LinearGroup; groups=() links none."""
     lib = lib or rans.build()
     done = []
     for name, child in list(module.named_modules()):
-        for cname, sub in list(child.named_children()):
+        children = dict(child.named_children())
+
+        def eligible(cname):
+            sub = children.get(cname)
             full = f"{name}.{cname}" if name else cname
-            if not isinstance(sub, torch.nn.Linear) or any(s in full for s in skip):
+            return (isinstance(sub, torch.nn.Linear) and not any(s in full for s in skip)
+                    and sub.in_features % 64 == 0)
+
+        tilings, links = {}, []
+        for names_ in groups or ():
+            if not all(eligible(n) for n in names_):
                 continue
-            if sub.in_features % 64:
+            subs = [children[n] for n in names_]
+            if len({s.in_features for s in subs}) != 1:
                 continue
-            setattr(child, cname, RansLinear.from_linear(sub, bits, lib, tune=tune))
+            try:
+                R, C = rans.pick_group_tiling([s.out_features for s in subs], subs[0].in_features)
+            except AssertionError:  # no compiled tile height divides every member
+                continue
+            for n in names_:
+                tilings[n] = (R, C, 1)
+            links.append(names_)
+        for cname in list(children):
+            if not eligible(cname):
+                continue
+            full = f"{name}.{cname}" if name else cname
+            new = RansLinear.from_linear(children[cname], bits, lib, tiling=tilings.get(cname),
+                                         tune=tune)
+            setattr(child, cname, new)
             done.append(full)
+        for names_ in links:
+            group = LinearGroup([getattr(child, n) for n in names_])
+            for m in group.members:
+                m.group = group
     return done
