@@ -1,6 +1,9 @@
 """Usage:
   python vram-compression_amd/rans_bench.py test    # correctness on small shapes
   python vram-compression_amd/rans_bench.py bench   # timing sweep, JSON report
+  python vram-compression_amd/rans_bench.py configs # the benchmark configurations
+  python vram-compression_amd/rans_bench.py chain [grouped|separate|both] [LAYERS]
+  python vram-compression_amd/rans_bench.py profile [ROWS COLS BITS DIST ESC R C N FETCH]
 
 Mirror of kernel/bench.py of snuri00/vram-compression (same function names
 and record keys, bench.py:20-126) for the w64 GEMV, plus the synthetic
@@ -444,5 +447,12 @@ if __name__ == "__main__":
     if sys.argv[1] == "profile":
         types = (int, int, float, str, float, int, int, int, str)
         profile(*(t(v) for t, v in zip(types, sys.argv[2:])))
+    elif sys.argv[1] == "chain":  # chain [grouped|separate|both] [layers]
+        mode = sys.argv[2] if len(sys.argv) > 2 else "both"
+        layers = int(sys.argv[3]) if len(sys.argv) > 3 else 28
+        for grouped in {"grouped": (True,), "separate": (False,)}.get(mode, (False, True)):
+            r = chain(layers=layers, grouped=grouped)
+            print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
+                              for k, v in r.items()}), flush=True)
     else:
         {"test": test, "bench": bench, "configs": configs}[sys.argv[1]]()
