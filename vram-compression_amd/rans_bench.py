@@ -2,7 +2,7 @@
   python vram-compression_amd/rans_bench.py test    # correctness on small shapes
   python vram-compression_amd/rans_bench.py bench   # timing sweep, JSON report
   python vram-compression_amd/rans_bench.py configs # the benchmark configurations
-  python vram-compression_amd/rans_bench.py chain [grouped|separate|both] [LAYERS]
+  python vram-compression_amd/rans_bench.py chain [grouped|separate|both] [LAYERS] [BATCH]
   python vram-compression_amd/rans_bench.py profile [ROWS COLS BITS DIST ESC R C N FETCH]
 
 Mirror of kernel/bench.py of snuri00/vram-compression (same function names
@@ -303,7 +303,7 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
 CHAIN_GROUPS = {"q": "qkv", "k": "qkv", "v": "qkv", "gate": "mlp", "up": "mlp"}
 
 
-def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False):
+def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False, batch=1):
     """Per-token chain of 7*layers batch-1 GEMVs over a random-init
     Qwen2.5-1.5B-shaped weight set (one table per matrix, ECSQ-like Laplace
     codes at `bits` bits/weight), graph-captured and replayed; the same chain
@@ -312,7 +312,8 @@ def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False):
     grouped: q, k, v and gate, up of a layer each run as one grouped launch
     (gemv_group, tiled with pick_group_tiling); the bf16 chain then runs q, k,
     v as one F.linear over the concatenated weights (faster than three),
-    gate and up separately (the concatenated shape is slower in rocBLAS)."""
+    gate and up separately (the concatenated shape is slower in rocBLAS).
+    batch: rows of x per GEMV (the same weights serve every row)."""
     lib = rans.build()
     rng = np.random.default_rng(seed)
     mats, Ws, xs = [], [], {}
@@ -359,10 +360,10 @@ def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False):
             nweights += codes.size
             Ws.append((torch.from_numpy(codes.astype(np.float32)) * step).bfloat16().cuda())
             if cols not in xs:
-                xs[cols] = torch.randn(cols, device="cuda").bfloat16()
+                xs[cols] = torch.randn(batch, cols, device="cuda").bfloat16()
             print(f"chain: layer {layer} {name} encoded", file=sys.stderr, flush=True) \
                 if name == "down" and layer % 7 == 0 else None
-    ys = {n: torch.empty(r, device="cuda") for n, r, _ in shapes}
+    ys = {n: torch.empty(batch, r, device="cuda") for n, r, _ in shapes}
     if grouped:  # q, k, v weights of a layer concatenated for the bf16 chain
         Wl, i = [], 0
         for step_ in steps:
@@ -388,8 +389,8 @@ def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False):
 
     t_rans = timeit_graph(run_rans, iters, warmup=2)
     t_bf16 = timeit_graph(run_bf16, iters, warmup=2)
-    return dict(config="Qwen2.5-1.5B-shaped weight set, 28 layers x 7 matrices, batch 1"
-                + (", q/k/v and gate/up grouped" if grouped else ""),
+    return dict(config=f"Qwen2.5-1.5B-shaped weight set, {layers} layers x 7 matrices, "
+                f"batch {batch}" + (", q/k/v and gate/up grouped" if grouped else ""),
                 gemvs=len(mats), launches=len(steps), weights=nweights, bits_target=bits,
                 bits_total=8 * nbytes / nweights, compressed_MB=nbytes / 1e6,
                 bf16_MB=nweights * 2 / 1e6, t_rans_us=t_rans, t_bf16_us=t_bf16,
@@ -447,11 +448,12 @@ if __name__ == "__main__":
     if sys.argv[1] == "profile":
         types = (int, int, float, str, float, int, int, int, str)
         profile(*(t(v) for t, v in zip(types, sys.argv[2:])))
-    elif sys.argv[1] == "chain":  # chain [grouped|separate|both] [layers]
+    elif sys.argv[1] == "chain":  # chain [grouped|separate|both] [layers] [batch]
         mode = sys.argv[2] if len(sys.argv) > 2 else "both"
         layers = int(sys.argv[3]) if len(sys.argv) > 3 else 28
+        batch = int(sys.argv[4]) if len(sys.argv) > 4 else 1
         for grouped in {"grouped": (True,), "separate": (False,)}.get(mode, (False, True)):
-            r = chain(layers=layers, grouped=grouped)
+            r = chain(layers=layers, grouped=grouped, batch=batch)
             print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
                               for k, v in r.items()}), flush=True)
     else:
