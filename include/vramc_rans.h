@@ -176,6 +176,11 @@ int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off, uin
                           uint32_t* states, uint32_t* table, int64_t* freq,
                           int32_t* esc_tileptr, int32_t* esc_pos, int32_t* esc_val);
 
+/* The symbol counts over the encoded matrix (256 x int64, symbol = code+128,
+ * 0 for escapes), for the bit accounting.  No reference counterpart (the
+ * reference recounts with numpy, rans.py:95-97). */
+int rans_w64_encode_counts(void* handle, int64_t* counts);
+
 void rans_w64_encode_free(void* handle);
 
 /* Host decoder of the w64 format to int32 codes (escapes applied); replaces

@@ -216,6 +216,24 @@ def test_bit_accounting(rans, oracle):
     assert enc["bits_table"] == 32 * 4096 / N
     assert 0 < pad <= 8 * ntiles
     assert np.all(np.diff(enc["tile_off"].astype(np.int64)) % 8 == 0)
+    # model entropy (from the encoder's symbol counts) against the direct mean
+    direct = -np.log2(freq[sym.ravel()] / 4096).mean()
+    assert abs(enc["entropy_model"] - direct) < 1e-9
+
+
+def test_encoder_threads_identical(rans, oracle):
+    """The threaded encoder (parallel symbol mapping, histogram and tiles)
+    gives the same stream for any thread count, escapes included."""
+    codes = oracle.synth_codes(1536, 1024, 3.25, seed=21)
+    rng = np.random.default_rng(21)
+    hit = rng.random(codes.shape) < 0.003
+    codes[hit] = rng.integers(128, 900, size=int(hit.sum()))
+    a = rans.encode(codes, 8, 512, 1, threads=1)
+    for th in (3, 8):
+        b = rans.encode(codes, 8, 512, 1, threads=th)
+        for k in ("words", "tile_off", "slen", "states", "table", "esc_tileptr", "esc_pos", "esc_val"):
+            np.testing.assert_array_equal(a[k], b[k])
+        assert a["entropy_model"] == b["entropy_model"]
 
 
 def test_bench_generators(rans, oracle, golden):

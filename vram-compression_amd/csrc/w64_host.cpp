@@ -5,6 +5,7 @@
 // The coder arithmetic is the reference's (kernel/rans.py:13-16, 62-98,
 // 101-123); the layout is this library's (see include/vramc_rans.h).
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -28,6 +29,7 @@ struct Encoded {
     std::vector<uint32_t> states;
     uint32_t table[kM];
     int64_t freq[256];
+    int64_t counts[256] = {0};  // symbol counts over the matrix
     std::vector<int32_t> esc_tileptr, esc_pos, esc_val;
     int64_t payload_words = 0;
     int32_t max_tile_words = 0;
@@ -54,11 +56,12 @@ void parallel_for(int64_t n, int nthreads, F fn) {
 
 }  // namespace
 
-extern "C" int rans_build_table(const uint8_t* sym, int64_t n, int64_t* freq, int64_t* cum,
-                                uint32_t* table) {
-    if (n <= 0 || !sym) return RANS_ECODES;
-    int64_t counts[256] = {0};
-    for (int64_t i = 0; i < n; i++) counts[sym[i]]++;
+namespace {
+
+// The table from symbol counts (n = their sum).
+int table_from_counts(const int64_t* counts, int64_t n, int64_t* freq, int64_t* cum,
+                      uint32_t* table) {
+    if (n <= 0) return RANS_ECODES;
     // Same quantisation as rans.py:36-44: round-half-even of count*M/total in
     // double precision, floor of 1 for present symbols, then move the rounding
     // residue onto the first largest bin.
@@ -93,6 +96,16 @@ extern "C" int rans_build_table(const uint8_t* sym, int64_t n, int64_t* freq, in
     return 0;
 }
 
+}  // namespace
+
+extern "C" int rans_build_table(const uint8_t* sym, int64_t n, int64_t* freq, int64_t* cum,
+                                uint32_t* table) {
+    if (n <= 0 || !sym) return RANS_ECODES;
+    int64_t counts[256] = {0};
+    for (int64_t i = 0; i < n; i++) counts[sym[i]]++;
+    return table_from_counts(counts, n, freq, cum, table);
+}
+
 extern "C" int rans_table_lds(const uint32_t* table, uint32_t* out) {
     if (!table || !out) return RANS_EARG;
     for (uint32_t i = 0; i < kM; i++) {
@@ -115,15 +128,29 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
     const int64_t N = (int64_t)rows * cols;
     auto* E = new Encoded();
 
-    // Symbols; the escape side table is collected per tile below.
+    // Symbols and their counts, in parallel over row blocks (per-block
+    // histograms summed in block order); the escape side table is collected
+    // per tile below.
     std::vector<uint8_t> sym((size_t)N);
-    for (int64_t i = 0; i < N; i++) {
-        const int32_t v = codes[i];
-        sym[(size_t)i] = v >= -127 && v <= 127 ? (uint8_t)(v + 128) : (uint8_t)kEsc;
-    }
+    const int nth = nthreads > 0 ? nthreads : 1;
+    const int64_t nblk = std::min<int64_t>((int64_t)nth * 4, rows);
+    std::vector<std::array<int64_t, 256>> hist((size_t)nblk);
+    parallel_for(nblk, nth, [&](int64_t b) {
+        std::array<int64_t, 256>& h = hist[(size_t)b];
+        h.fill(0);
+        const int64_t lo = (int64_t)rows * b / nblk * cols, hi = (int64_t)rows * (b + 1) / nblk * cols;
+        for (int64_t i = lo; i < hi; i++) {
+            const int32_t v = codes[i];
+            const uint8_t y = v >= -127 && v <= 127 ? (uint8_t)(v + 128) : (uint8_t)kEsc;
+            sym[(size_t)i] = y;
+            h[y]++;
+        }
+    });
+    for (const auto& h : hist)
+        for (int y = 0; y < 256; y++) E->counts[y] += h[(size_t)y];
 
     int64_t cum[256];
-    if (rans_build_table(sym.data(), N, E->freq, cum, E->table) != 0) {
+    if (table_from_counts(E->counts, N, E->freq, cum, E->table) != 0) {
         delete E;
         return RANS_ECODES;
     }
@@ -277,6 +304,12 @@ extern "C" int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* ti
     put(esc_val, E->esc_val);
     if (table) std::memcpy(table, E->table, sizeof(E->table));
     if (freq) std::memcpy(freq, E->freq, sizeof(E->freq));
+    return 0;
+}
+
+extern "C" int rans_w64_encode_counts(void* handle, int64_t* counts) {
+    if (!handle || !counts) return RANS_EARG;
+    std::memcpy(counts, static_cast<Encoded*>(handle)->counts, sizeof(int64_t) * 256);
     return 0;
 }
 

@@ -64,7 +64,8 @@ class RansMatrixDesc(ctypes.Structure):
 EXPORTS = ("launch_rans_gemv", "rans_gemv_workspace_bytes", "launch_rans_gemv_group",
            "launch_rans_decode",
            "launch_rans_decode_codes", "launch_int4_gemv", "rans_build_table", "rans_table_lds",
-           "rans_w64_encode", "rans_w64_encode_fetch", "rans_w64_encode_free",
+           "rans_w64_encode", "rans_w64_encode_fetch", "rans_w64_encode_counts",
+           "rans_w64_encode_free",
            "rans_w64_decode_host")
 
 
@@ -102,6 +103,7 @@ def load_lib(path=LIB):
         "rans_table_lds": ([P, P], ctypes.c_int),
         "rans_w64_encode": ([P, I32, I32, I32, I32, I32, I32, ctypes.POINTER(P), P], ctypes.c_int),
         "rans_w64_encode_fetch": ([P] * 10, ctypes.c_int),
+        "rans_w64_encode_counts": ([P, P], ctypes.c_int),
         "rans_w64_encode_free": ([P], None),
         "rans_w64_decode_host": ([D, P], ctypes.c_int),
     }
@@ -204,16 +206,19 @@ def encode(codes, R, C, S=1, threads=None):
     esc_tileptr = np.zeros(ntiles + 1, np.int32)
     esc_pos = np.zeros(nesc, np.int32)
     esc_val = np.zeros(nesc, np.int32)
+    counts = np.zeros(256, np.int64)
     try:
         rc = lib.rans_w64_encode_fetch(h, _p(words), _p(tile_off), _p(slen), _p(states),
                                        _p(table), _p(freq), _p(esc_tileptr), _p(esc_pos),
                                        _p(esc_val))
         assert rc == 0
+        assert lib.rans_w64_encode_counts(h, _p(counts)) == 0
     finally:
         lib.rans_w64_encode_free(h)
     N = codes.size
-    sym = np.where((codes >= -127) & (codes <= 127), codes + OFFSET, ESC).astype(np.uint8)
-    p = freq[sym.ravel()] / M
+    # model entropy: -mean log2 p over the symbols, from the counts
+    present = counts > 0
+    entropy_model = float(-(counts[present] * np.log2(freq[present] / M)).sum() / N)
     pad_words = nwords - payload_words
     return dict(words=words, tile_off=tile_off, slen=slen, states=states, table=table,
                 esc_tileptr=esc_tileptr, esc_pos=esc_pos, esc_val=esc_val,
@@ -223,7 +228,7 @@ def encode(codes, R, C, S=1, threads=None):
                 bits_state_offs=(40 * nstates + 32 * (ntiles + 1) + 16 * pad_words) / N,
                 bits_table=32 * M / N,
                 bits_escape=32 * (ntiles + 1 + 2 * nesc) / N,
-                entropy_model=float(-np.log2(p).mean()))
+                entropy_model=entropy_model)
 
 
 def pick_tiling(rows, cols, R=None, S=1, target_states=None, max_ncb=None):
