@@ -323,7 +323,10 @@ extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
     const int32_t ncb = cols / C, nrb = rows / R, nst = 64 * S, nk = C / nst;
     const int64_t ntiles = (int64_t)nrb * ncb;
     const int64_t nwords = m->tile_off[ntiles];
-    for (int64_t t = 0; t < ntiles; t++) {
+    // Tiles decode independently, on up to 16 threads; each stops at its
+    // first failure, and the failure of the lowest tile is returned (what a
+    // tile-by-tile decode would return).
+    auto decode_tile = [&](int64_t t) -> int {
         const int32_t rb = (int32_t)(t / ncb), cb = (int32_t)(t % ncb);
         int64_t start = m->tile_off[t];  // streams follow each other in state order
         for (int32_t j = 0; j < nst; j++) {
@@ -348,7 +351,13 @@ extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
             if (p - start != m->slen[sid]) return RANS_EARG;
             start = p;
         }
-    }
+        return 0;
+    };
+    std::vector<int> err((size_t)ntiles, 0);
+    const int nth = (int)std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency()));
+    parallel_for(ntiles, nth, [&](int64_t t) { err[(size_t)t] = decode_tile(t); });
+    for (int64_t t = 0; t < ntiles; t++)
+        if (err[(size_t)t]) return err[(size_t)t];
     // The escape symbol decodes to kEsc-128; the side table must name exactly
     // those positions: the same count, each entry inside its tile on an
     // escape symbol, strictly ascending within the tile (so none twice).
