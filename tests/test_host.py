@@ -126,6 +126,23 @@ def test_corrupt_state_detected(rans, oracle):
         oracle.w64_decode(bad)
 
 
+def test_first_failing_tile_is_reported(rans, oracle):
+    """With two corrupted tiles the host decoder (tiles decoded in parallel)
+    reports the lower tile's state, as a tile-by-tile decode does."""
+    import ctypes
+    codes = oracle.synth_codes(256, 1024, 3.0, seed=17)
+    enc = rans.encode(codes, 8, 256, 1)
+    nst = 64
+    bad = dict(enc, states=enc["states"].copy())
+    bad["states"][9 * nst + 5] ^= 0x1234   # tile 9, state 5
+    bad["states"][3 * nst + 40] ^= 0x777   # tile 3, state 40: reported
+    keep = []
+    d = rans._host_desc(bad, keep)
+    out = np.zeros(codes.shape, np.int32)
+    rc = rans._host_lib().rans_w64_decode_host(ctypes.byref(d), rans._p(out))
+    assert rc == 3 * nst + 40 + 1
+
+
 def test_encode_rejects_bad_input(rans):
     ok = np.random.default_rng(0).integers(-3, 4, size=(16, 128)).astype(np.int32)
     with pytest.raises(AssertionError):
