@@ -192,6 +192,8 @@ def main():
     ap.add_argument("--word-fetch", choices=("tune", "always", "refill"), default="tune",
                     help="GEMV word-fetch policy; 'tune' times both on the matrix")
     ap.add_argument("--no-rocblas", action="store_true")
+    ap.add_argument("--no-chain", action="store_true",
+                    help="skip the per-token chain (196 GEMVs, grouped launches)")
     ap.add_argument("--sweep", action="store_true", help="print a tiling sweep to stderr")
     ap.add_argument("--profile", action="store_true",
                     help="for rocprofv3: K eager launches of the headline GEMV over the rotating "
@@ -312,6 +314,18 @@ def main():
 
     cpu = None if args.no_cpu else cpu_baseline(codes, step, torch.from_numpy(x).bfloat16().float().numpy())
 
+    # The per-token chain of a Qwen2.5-1.5B-shaped weight set (28 layers x 7
+    # matrices at 3.25 bits, batch 1), each layer's q/k/v and gate/up as one
+    # grouped launch, against the bf16 chain with q/k/v concatenated.
+    chain = None
+    if not args.no_chain:
+        r = B.chain(grouped=True)
+        chain = {"us_per_token": r["t_rans_us"], "bf16_us_per_token": r["t_bf16_us"],
+                 "speedup_vs_bf16": r["speedup_vs_bf16"], "launches": r["launches"],
+                 "gemvs": r["gemvs"], "bits_total": r["bits_total"],
+                 "workload": r["config"]}
+        torch.cuda.empty_cache()
+
     achieved = alg / (t_rot * 1e-6) / 1e9
     fetch_name = {rans.F_WORDS_ALWAYS: "always", rans.F_WORDS_REFILL: "refill"}.get(measure.flags & 3)
     pmc = PMC_TRAFFIC_KIB.get((R, C, S, fetch_name))
@@ -349,6 +363,7 @@ def main():
                      "(profiles/rans_w64_gemv_1536x8960_3.25b.md)",
                      "kernel": "rans_w64_gemv_kernel", "bytes_per_launch": alg},
         "cpu_baseline": cpu,
+        "chain": chain,
     }
     print(json.dumps(out), flush=True)
 
