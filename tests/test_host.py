@@ -271,3 +271,21 @@ def test_bench_generators(rans, oracle, golden):
         for S in (1, 2):
             R, C = B.pick_tiling(rows, cols, S=S)
             assert rows % R == 0 and cols % C == 0 and C % (64 * S) == 0
+
+
+def test_w64_format_golden(rans):
+    """The encoder's exact output on the committed fixture (escapes, two
+    states per lane, 35-row tiles): a change to the stream bytes is a
+    format change.  tests/golden/make_w64_golden.py wrote the fixture."""
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "w64_format_vectors.npz")
+    g = np.load(path)
+    for name in ("esc", "s2", "r35"):
+        rows, cols, R, C, S, mtw, msw = (int(v) for v in g[f"{name}_meta"])
+        codes = g[f"{name}_codes"].astype(np.int32)
+        assert codes.shape == (rows, cols)
+        enc = rans.encode(codes, R, C, S)
+        for k in ("words", "tile_off", "slen", "states", "table", "esc_tileptr", "esc_pos", "esc_val"):
+            np.testing.assert_array_equal(enc[k], g[f"{name}_{k}"], err_msg=f"{name}.{k}")
+        assert (enc["max_tile_words"], enc["max_state_words"]) == (mtw, msw)
+        np.testing.assert_array_equal(rans.decode_ref(enc), codes)
