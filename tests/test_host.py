@@ -285,7 +285,7 @@ def test_w64_format_golden(rans):
         codes = g[f"{name}_codes"].astype(np.int32)
         assert codes.shape == (rows, cols)
         enc = rans.encode(codes, R, C, S)
-        for k in ("words", "tile_off", "slen", "states", "table", "esc_tileptr", "esc_pos", "esc_val"):
+        for k in ("words", "tile_off", "slen", "states", "esc_tileptr", "esc_pos", "esc_val"):
             np.testing.assert_array_equal(enc[k], g[f"{name}_{k}"], err_msg=f"{name}.{k}")
         assert (enc["max_tile_words"], enc["max_state_words"]) == (mtw, msw)
         np.testing.assert_array_equal(rans.decode_ref(enc), codes)
