@@ -132,3 +132,39 @@ def test_linear_group_reuses_one_launch(rans, lib):
         assert len(calls) == 4
     finally:
         rans.gemv_group = real
+
+
+def test_linear_group_prefill_one_gemm(rans, lib):
+    """Prefill-sized inputs (more than 8 rows) through a LinearGroup: the
+    members' weights are decoded into one bf16 matrix and one dense GEMM
+    serves all three calls.  Each output is within the prefill bar (1e-2)
+    of the float64 product with code*step, and within 5e-3 of the member's
+    own decode + GEMM (both round the GEMM's output to bf16, and the two
+    GEMM shapes may round an element differently)."""
+    import rans_linear as L
+    print("case LinearGroup prefill q/k/v 1536+256+256 x 1536, 12 rows", flush=True)
+    g = torch.Generator().manual_seed(9)
+    R, C = rans.pick_group_tiling([1536, 256, 256], 1536)
+    mods = []
+    for rows in (1536, 256, 256):
+        codes, step = L.quantize_uniform(torch.randn(rows, 1536, generator=g) * 0.02, 3.5)
+        mods.append(L.RansLinear.from_codes(codes, step, torch.randn(rows, generator=g), lib,
+                                            tiling=(R, C, 1), tune=False))
+    group = L.LinearGroup(mods)
+    for m in mods:
+        m.group = group
+    x = torch.randn(12, 1536, generator=g).bfloat16().cuda()
+    calls = []
+    real = torch.nn.functional.linear
+    torch.nn.functional.linear = lambda *a, **k: (calls.append(1), real(*a, **k))[1]
+    try:
+        ys = [m(x) for m in mods]
+    finally:
+        torch.nn.functional.linear = real
+    assert len(calls) == 1
+    for m, y in zip(mods, ys):
+        own = torch.nn.functional.linear(x, m.matrix.decode()).float() + m.bias
+        wd = m.matrix.decode_codes().double() * m.matrix.step.double().reshape(1, -1)
+        ref = x.double() @ wd.t() + m.bias.double()
+        assert _rel(y, ref) <= 1e-2
+        assert _rel(y.float(), own) <= 5e-3

@@ -59,13 +59,15 @@ def quantize_uniform(weight, bits, iters=40, sample=1 << 22, seed=0):
 
 class LinearGroup:
     """RansLinear modules that read the same input: a decoder layer's q, k
-    and v projections, or its gate and up.  When a member is called (with a
-    decode-sized input), every member's product is computed in one grouped
-    launch (rans.gemv_group); the other members' results are kept and
-    returned when those members are called with the same input tensor,
-    unmodified, so Hugging Face's q_proj(h), k_proj(h), v_proj(h) costs one
-    launch.  A member called with any other input computes afresh.  The
-    members need the same tiling (rans.pick_group_tiling)."""
+    and v projections, or its gate and up.  When a member is called, every
+    member's product is computed at once: for decode-sized inputs in one
+    grouped launch (rans.gemv_group), for larger ones by decoding all
+    members into one bf16 weight and one dense GEMM.  The other members'
+    results are kept and returned when those members are called with the
+    same input tensor, unmodified, so Hugging Face's q_proj(h), k_proj(h),
+    v_proj(h) costs one launch (or one GEMM).  A member called with any
+    other input computes afresh.  The members need the same tiling
+    (rans.pick_group_tiling) for the grouped launch."""
 
     def __init__(self, members):
         self.members = list(members)
@@ -75,12 +77,26 @@ class LinearGroup:
 
     def product(self, member, x, xd):
         """member's x @ W^T (no bias) for the module input x, flattened and
-        converted to xd (rows x in_features, f32 or bf16)."""
+        converted to xd (rows x in_features, f32 or bf16); f32."""
         i = next(j for j, m in enumerate(self.members) if m is member)
         if (self._x is not None and self._x() is x and self._version == x._version
                 and i in self._pending):
             return self._pending.pop(i)
-        ys = rans.gemv_group([m.matrix for m in self.members], xd)
+        if xd.shape[0] > PREFILL_ROWS:
+            # all members decoded into row slices of one bf16 weight, one GEMM
+            w = torch.empty(sum(m.out_features for m in self.members), xd.shape[1],
+                            device="cuda", dtype=torch.bfloat16)
+            ys, off = [], 0
+            for m in self.members:
+                m.matrix.decode(w[off:off + m.out_features])
+                off += m.out_features
+            yall = torch.nn.functional.linear(xd.to(torch.bfloat16), w).float()
+            off = 0
+            for m in self.members:
+                ys.append(yall[:, off:off + m.out_features])
+                off += m.out_features
+        else:
+            ys = rans.gemv_group([m.matrix for m in self.members], xd)
         self._x, self._version = weakref.ref(x), x._version
         self._pending = {j: y for j, y in enumerate(ys) if j != i}
         return ys[i]
@@ -132,11 +148,11 @@ class RansLinear(torch.nn.Module):
         xd = x.reshape(-1, self.in_features)
         if xd.dtype not in (torch.bfloat16, torch.float32):
             xd = xd.float()
-        if xd.shape[0] > PREFILL_ROWS:
+        if self.group is not None:
+            y = self.group.product(self, x, xd.contiguous())
+        elif xd.shape[0] > PREFILL_ROWS:
             w = self.matrix.decode()  # bf16 code*step, then the dense GEMM
             y = torch.nn.functional.linear(xd.to(torch.bfloat16), w).float()
-        elif self.group is not None:
-            y = self.group.product(self, x, xd.contiguous())
         else:
             y = self.matrix.gemv(xd.contiguous())
         if self.bias is not None:
