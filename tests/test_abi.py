@@ -118,3 +118,22 @@ def test_oracle_is_not_imported_by_the_product():
             if f.endswith((".py", ".hip", ".cpp", ".h")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "import oracle" not in text and "liboracle" not in text, f
+
+
+def test_header_compiles_as_c(tmp_path):
+    """include/vramc_rans.h is plain C for non-Python bindings (cgo, JNI,
+    a C caller): it compiles as C99 and as C++17."""
+    import os
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None or not os.path.isdir("/opt/rocm/include"):
+        pytest.skip("needs gcc and the ROCm headers")
+    inc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+    src = tmp_path / "use.c"
+    src.write_text('#include "vramc_rans.h"\n'
+                   "int main(void) { rans_w64_matrix m = {0}; (void)m;\n"
+                   "  return launch_rans_gemv_group ? 0 : 1; }\n")
+    for std, lang in (("c99", "c"), ("c++17", "c++")):
+        subprocess.check_call([gcc, f"-std={std}", "-x", lang, "-fsyntax-only", f"-I{inc}",
+                               "-I/opt/rocm/include", "-D__HIP_PLATFORM_AMD__", str(src)])
