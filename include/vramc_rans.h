@@ -80,6 +80,14 @@ extern "C" {
 #define RANS_F_WORDS_MASK 3
 #define RANS_F_NO_ESCAPES 4   /* the side table is empty: kernels skip it (a promise; a
                                  matrix with escapes decodes them as 0 under this flag) */
+/* Table entries of the GEMV (bits 3-4; same results, different speed).  With
+ * neither flag the library picks: the 4-byte entries (table_lds4, when set)
+ * for a batch-1 launch with S = 1 whose workgroups do not all fit on the chip
+ * at once with the 8-byte ones, else the 8-byte entries (table_lds).  Grouped
+ * launches and the decode kernels always use the 8-byte entries. */
+#define RANS_F_TABLE8 8       /* always the 8-byte entries */
+#define RANS_F_TABLE4 16      /* always the 4-byte entries: needs table_lds4 (else
+                                 RANS_EARG) and S = 1 (else RANS_EUNSUPPORTED) */
 
 typedef struct rans_w64_matrix {
     int32_t rows, cols;       /* out_features, in_features */
@@ -101,6 +109,8 @@ typedef struct rans_w64_matrix {
     const float* step;        /* [cols] per-column step (waterfilling) */
     void* workspace;          /* split-K partials + counters; zero-filled once */
     int64_t workspace_bytes;
+    const uint32_t* table_lds4;/* [4096] or NULL: the table as 4-byte LDS entries, made by
+                                 rans_table_lds4 (GEMV only; see RANS_F_TABLE4) */
 } rans_w64_matrix;
 
 /* ---------------------------------------------------------------- device */
@@ -112,6 +122,14 @@ typedef struct rans_w64_matrix {
  * which takes a host-folded f32 x and needs y zeroed when cols != C. */
 int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
                      void* y, hipStream_t stream);
+
+/* 1 when launch_rans_gemv at this batch and x dtype would run any of its
+ * launches with the 4-byte table entries, were table_lds4 set (0 if not, or
+ * a negative RANS_E* for arguments it would reject).  A caller asks before
+ * building the 16 KB image, which only such matrices need.  Uses the
+ * current device's occupancy figures; launches nothing.  No reference
+ * counterpart. */
+int rans_gemv_table4(const rans_w64_matrix* m, int x_dtype, int batch);
 
 /* Bytes of workspace launch_rans_gemv needs for this matrix and batch (0 when
  * one workgroup covers a whole tile row).  The first 4096 bytes are counters
@@ -160,6 +178,11 @@ int rans_build_table(const uint8_t* sym, int64_t n, int64_t* freq, int64_t* cum,
  * the fields on every symbol (rans_gemv.cu:33-36).  Returns RANS_EARG for a
  * null pointer. */
 int rans_table_lds(const uint32_t* table, uint32_t* out);
+
+/* The 4-byte LDS image: out[slot] = freq | (slot-cum)<<12 | code<<24 (code as
+ * in rans_table_lds), 16 KB.  No reference counterpart.  Returns RANS_EARG
+ * for a null pointer. */
+int rans_table_lds4(const uint32_t* table, uint32_t* out);
 
 /* Encode int32 codes (rows x cols, row-major) into the w64 format; replaces
  * encode() (rans.py:62-98).  R <= 256 and C < 2^23 (the side table's

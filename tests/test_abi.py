@@ -59,10 +59,29 @@ def test_argument_validation_without_gpu(rans, lib):
     assert lib.rans_gemv_workspace_bytes(ctypes.byref(one), 1) == 0
     huge = _desc(rans, mtw=70000)
     assert lib.rans_gemv_workspace_bytes(ctypes.byref(huge), 1) == -2
-    for flags in (3, 8, -1):  # both word-fetch bits, or an unknown bit
+    for flags in (3, 24, 32, -1):  # both word-fetch bits, both table bits, an unknown bit
         bad_flags = _desc(rans, cols=2048)
         bad_flags.flags = flags
         assert lib.launch_rans_gemv(ctypes.byref(bad_flags), x, 0, 1, y, None) == -2
+        assert lib.rans_gemv_table4(ctypes.byref(bad_flags), 0, 1) == -2
+    # the 4-byte table entries, forced: they need their image and one state per lane
+    t4 = _desc(rans, cols=2048)
+    t4.flags = rans.F_TABLE4
+    assert lib.launch_rans_gemv(ctypes.byref(t4), x, 0, 1, y, None) == -4
+    t4s2 = _desc(rans, cols=2048, S=2)
+    t4s2.flags = rans.F_TABLE4
+    t4s2.table_lds4 = 0x1000
+    assert lib.launch_rans_gemv(ctypes.byref(t4s2), x, 0, 1, y, None) == -1
+    assert lib.rans_gemv_table4(ctypes.byref(t4s2), 0, 1) == -1
+    # forced choices are answered without the occupancy query
+    t4.table_lds4 = 0x1000
+    assert lib.rans_gemv_table4(ctypes.byref(t4), 1, 1) == 1
+    t8 = _desc(rans, cols=2048)
+    t8.flags = rans.F_TABLE8
+    assert lib.rans_gemv_table4(ctypes.byref(t8), 1, 1) == 0
+    assert lib.rans_gemv_table4(ctypes.byref(t8), 7, 1) == -4
+    assert lib.rans_gemv_table4(ctypes.byref(t8), 1, 0) == -2
+    assert lib.rans_table_lds4(None, y) == -4
     no_img = _desc(rans)
     no_img.table_lds = None  # the kernels need the table's LDS image
     assert lib.launch_rans_gemv(ctypes.byref(no_img), x, 0, 1, y, None) == -4

@@ -4,6 +4,8 @@ Bars: decoded codes bit-exact; bf16 decode bit-exact against
 bf16(code*step) (round to nearest even); GEMV relative L2 <= 1e-3 against the
 oracle's float64 dequant+GEMV (and, on the reference's own test shapes, its
 max-abs-relative < 1e-4 criterion, kernel/bench.py:55-56)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -293,6 +295,16 @@ def test_full_size_27b_shapes(rans, oracle, lib, dev, rows, cols):
     assert torch.equal(m.gemv(x).cpu(), y4)
     assert _rel_l2(y4.numpy(), ref) <= REL_L2
     assert _rel_l2(y1.numpy(), ref[0]) <= REL_L2
+    # more workgroups than the chip holds at once: batch 1 runs on the
+    # 4-byte table entries, batch 4 on the 8-byte ones; forcing either
+    # layout changes no bit
+    assert m.table_lds4 is not None
+    assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, 1) == 1
+    assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, 4) == 0
+    m._desc.flags = rans.F_WORDS_REFILL | rans.F_TABLE8
+    assert torch.equal(m.gemv(x[0]).cpu(), y1)
+    m._desc.flags = rans.F_WORDS_REFILL | rans.F_TABLE4
+    assert torch.equal(m.gemv(x).cpu(), y4)
 
 
 def test_no_escape_flag(rans, oracle, lib, dev):
@@ -427,3 +439,46 @@ def test_r35_tiles(rans, oracle, lib, dev, rows, cols, C, batch):
         m2 = rans.RansMatrix(rans.encode(codes, 35, C, 2), torch.from_numpy(step), lib)
         with pytest.raises(AssertionError, match="HIP error -1"):
             m2.gemv(x)
+
+
+@pytest.mark.parametrize("R,C", [(1, 256), (2, 256), (3, 512), (4, 256), (8, 512), (16, 128),
+                                 (35, 192)])
+def test_table_entry_layouts_agree(rans, oracle, lib, dev, R, C):
+    """The 8-byte and the 4-byte LDS table entries decode the same symbols:
+    forced either way, GEMV outputs are bitwise equal at batch 1, 4 and 5
+    (f32 and bf16 x), escapes included, and match the oracle."""
+    rows, cols = 35 * 24 if R == 35 else 384, 1536
+    print(f"case table entries R={R} C={C}", flush=True)
+    codes = oracle.synth_codes(rows, cols, 3.25, seed=R * 7 + 1)
+    codes[3, 11] = 250  # escapes of both signs
+    codes[rows - 1, cols - 2] = -400
+    rng = np.random.default_rng(R)
+    step = np.exp(0.5 * rng.standard_normal(cols)).astype(np.float32)
+    enc = rans.encode(codes, R, C, 1)
+    m8 = rans.RansMatrix(enc, torch.from_numpy(step), lib, flags=rans.F_TABLE8)
+    m4 = rans.RansMatrix(enc, torch.from_numpy(step), lib, flags=rans.F_TABLE4)
+    assert m8.table_lds4 is None and m4.table_lds4 is not None
+    assert m4.nbytes == m8.nbytes + 16384
+    for batch in (1, 4, 5):
+        x = torch.from_numpy(rng.standard_normal((batch, cols)).astype(np.float32)).cuda()
+        for xt in (x, x.bfloat16()):
+            y8 = m8.gemv(xt).cpu()
+            y4 = m4.gemv(xt).cpu()
+            assert torch.equal(y8, y4), (batch, xt.dtype)
+        ref = oracle.gemv_f64(codes, x.bfloat16().float().cpu().numpy().astype(np.float64),
+                              step.astype(np.float64))
+        assert _rel_l2(y4.numpy(), ref) <= REL_L2
+
+
+def test_table_entries_choice(rans, lib, dev):
+    """The library keeps the 8-byte entries for launches whose workgroups
+    all fit on the chip at once (1536x8960 in 3x2240 tiles: 512
+    workgroups), and the wrapper then uploads no 4-byte image."""
+    import rans_bench as B
+    print("case table entry choice 1536x8960", flush=True)
+    codes = B.synth_codes_full(1536, 8960, 3.25, dist="laplace", seed=3)
+    enc = rans.encode(codes, 3, 2240, 1)
+    m = rans.RansMatrix(enc, torch.ones(8960), lib)
+    assert m.table_lds4 is None
+    for batch in (1, 4):
+        assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, batch) == 0

@@ -206,6 +206,33 @@ def test_table_lds_image(rans, oracle, golden):
     assert np.all(img[0::2] == 5) and np.all(img[1::2] == 3)
 
 
+def test_table_lds4_image(rans, oracle, golden):
+    """The 4-byte LDS entries: per slot of symbol y, freq[y] | (slot -
+    cum[y])<<12 | code<<24, rebuilt from freq/cum.  Decoding the fields as
+    the kernel does (mask, 12-bit extract, arithmetic shift) gives the
+    reference's next state freq*(x>>12) + (x & 4095) - cum for every slot."""
+    x = np.random.default_rng(1).integers(1 << 16, 1 << 32, size=4096, dtype=np.uint64)
+    for name in ["two_symbols", "tie_argmax", "laplace"]:
+        sym = golden[f"tab_{name}_sym"]
+        freq, cum, table = oracle.build_table(sym)
+        img = rans.table_lds4(table)
+        assert img.dtype == np.uint32 and img.size == 4096
+        for y in np.nonzero(freq)[0]:
+            code = 0 if y == 0 else int(y) - 128
+            slots = np.arange(cum[y], cum[y] + freq[y])
+            want = freq[y] | ((slots - cum[y]) << 12) | ((code & 0xFF) << 24)
+            np.testing.assert_array_equal(img[slots], want.astype(np.uint32))
+        xs = (x & ~np.uint64(0xFFF)) | np.arange(4096, dtype=np.uint64)  # state in every slot
+        e = img[np.arange(4096)].astype(np.uint64)
+        ns = (e & 0xFFF) * (xs >> 12) + ((e >> 12) & 0xFFF)
+        ys = np.nonzero(freq)[0]  # symbol of each slot: cum ascends with the symbol
+        s_of = ys[np.searchsorted(np.cumsum(freq[ys]), np.arange(4096), side="right")]
+        ref = freq[s_of].astype(np.uint64) * (xs >> 12) + (xs & 0xFFF) - cum[s_of].astype(np.uint64)
+        np.testing.assert_array_equal(ns, ref)
+        codes = img.view(np.int32) >> 24
+        np.testing.assert_array_equal(codes, np.where(s_of == 0, 0, s_of - 128))
+
+
 def test_lane_order_matches_oracle(rans, oracle):
     a = np.arange(32 * 1024).reshape(32, 1024)
     for R, C, S in [(1, 64, 1), (4, 256, 2), (8, 1024, 4), (32, 512, 1)]:

@@ -39,19 +39,27 @@ constexpr uint32_t kProbM = 4096;
 constexpr uint32_t kRansL = 1u << 16;
 constexpr int kMaxWaves = 8;
 
-// Table entry in LDS: {freq | code<<24, slot - cum}; one mad consumes both
-// words and the code is the sign-extended top byte.
-using TabEntry = uint2;
+// Table entry in LDS, in one of two layouts:
+//   - 8 bytes {freq | code<<24, slot - cum} (T4 = false): one mad consumes
+//     both words and the code is the sign-extended top byte;
+//   - 4 bytes freq | (slot - cum)<<12 | code<<24 (T4 = true): half the LDS
+//     and half the bytes per random table read, for two more VALU
+//     instructions per symbol (a mask and a field extract, one of them on
+//     the state's dependency chain).  It pays on batch-1 launches with more
+//     workgroups than the chip holds at once: the 16 KB saved per
+//     workgroup lets more of them share a CU.
+template <bool T4>
+using TabEntry = std::conditional_t<T4, uint32_t, uint2>;
 
 // LDS: the expanded table and the reduction scratch are static __shared__
 // arrays (their offsets are compile-time constants, so table addressing
 // needs no base add); the per-wave regions are dynamic.  The GEMV's
 // reduction scratch holds R*B floats per wave: the host reserves it for a
 // batch of 4 (the largest compiled), plus the 16-byte arrival flag.
-constexpr int gemv_static_lds(int R) {
-    return (int)sizeof(TabEntry) * (int)kProbM + 4 * kMaxWaves * R * 4 + 16;
+constexpr int gemv_static_lds(int R, bool t4 = false) {
+    return (t4 ? 4 : 8) * (int)kProbM + 4 * kMaxWaves * R * 4 + 16;
 }
-constexpr int kDecodeStaticLds = (int)sizeof(TabEntry) * (int)kProbM;
+constexpr int kDecodeStaticLds = (int)sizeof(TabEntry<false>) * (int)kProbM;
 constexpr int kLdsMax = 160 * 1024;
 constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3 for gfx9 raw loads
 
@@ -129,11 +137,19 @@ struct DecodeArgs {
 
 // freq*(st>>12) + bias (rans_gemv.cu:34): freq < 2^12 and st>>12 < 2^20
 // both fit the 24-bit multiplier, whose operand ignores the code byte.
-__device__ __forceinline__ uint32_t entry_next_state(TabEntry e, uint32_t st) {
+__device__ __forceinline__ uint32_t entry_next_state(uint2 e, uint32_t st) {
     return __umul24(e.x, st >> 12) + e.y;
 }
 
-__device__ __forceinline__ int32_t entry_code(TabEntry e) { return (int32_t)e.x >> 24; }
+__device__ __forceinline__ int32_t entry_code(uint2 e) { return (int32_t)e.x >> 24; }
+
+// The 4-byte entry: freq is masked out (the multiplier would take the bias
+// bits above it) and the bias extracted from bits 12..23.
+__device__ __forceinline__ uint32_t entry_next_state(uint32_t e, uint32_t st) {
+    return __umul24(e & 0xFFFu, st >> 12) + __builtin_amdgcn_ubfe(e, 12, 12);
+}
+
+__device__ __forceinline__ int32_t entry_code(uint32_t e) { return (int32_t)e >> 24; }
 
 // Direct global->LDS copy (global_load_lds_dwordx4): lane i's 16 bytes land
 // at the wave-uniform LDS address base + 16*i.  The copy is complete when
@@ -146,13 +162,16 @@ __device__ __forceinline__ void copy16_to_lds(const uint4* src_lane, void* lds_w
 // so the compiler's own wait tracking knows every vector load is complete.
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// The 32 KB table image: 32 chunks of 64 x 16 bytes, wave w of W copying
-// chunks w, w+W, ...  Issued after the tile block's copy: the table comes
-// from L2 (every workgroup reads it), the block from HBM, so the block's
-// copy is the one to start first.
-__device__ __forceinline__ void stage_table(TabEntry* tab, const uint4* __restrict__ img, int wave,
-                                            int W, int lane) {
-    for (int c = wave; c < 32; c += W)
+// The table image (32 KB of 8-byte or 16 KB of 4-byte entries, laid out as
+// in LDS): chunks of 64 x 16 bytes, wave w of W copying chunks w, w+W, ...
+// Issued after the tile block's copy: the table comes from L2 (every
+// workgroup reads it), the block from HBM, so the block's copy is the one
+// to start first.
+template <class E>
+__device__ __forceinline__ void stage_table(E* tab, const uint4* __restrict__ img, int wave, int W,
+                                            int lane) {
+    constexpr int nchunks = (int)(sizeof(E) * kProbM / 1024);
+    for (int c = wave; c < nchunks; c += W)
         copy16_to_lds(img + c * 64 + lane, reinterpret_cast<uint4*>(tab) + c * 64);
 }
 
@@ -320,18 +339,18 @@ __device__ __forceinline__ void stream_offsets(const uint32_t (&len)[S], uint32_
 // Per-lane decoder state of S interleaved rANS states, with the table entry
 // of each state's next symbol already read (software pipelined: the read for
 // symbol i+1 is issued before the GEMV work of symbol i).
-template <int S>
+template <int S, class E>
 struct Lanes {
     uint32_t st[S];  // rANS states
     uint32_t a[S];   // LDS byte address of the next unread word of each state
     uint32_t w[S];   // that word (read ahead)
-    TabEntry e[S];   // table entry for the next symbol of each state
+    E e[S];          // table entry for the next symbol of each state
 };
 
 // Staged-block setup: each state's read pointer, its first word and the
 // table entry of its first symbol.  Call after the staging barrier.
-template <int S>
-__device__ __forceinline__ void init_lanes(Lanes<S>& L, const TabEntry* tab, const uint16_t* raw,
+template <int S, class E>
+__device__ __forceinline__ void init_lanes(Lanes<S, E>& L, const E* tab, const uint16_t* raw,
                                            const uint32_t (&st0)[S], const uint32_t (&off0)[S]) {
 #pragma unroll
     for (int s = 0; s < S; s++) {
@@ -354,10 +373,10 @@ __device__ __forceinline__ void init_lanes(Lanes<S>& L, const TabEntry* tab, con
 // bottleneck).  REFILL=true: only the lanes that just consumed their word
 // fetch the next one (an EXEC-masked read, about 1 lane in 5 at 3 bits per
 // symbol), which cuts LDS bank traffic where many waves share the CU.
-template <bool REFILL>
-__device__ __forceinline__ int32_t rans_step(uint32_t& st, uint32_t& a, uint32_t& w, TabEntry& e,
-                                             const TabEntry* tab) {
-    const TabEntry cur = e;
+template <bool REFILL, class E>
+__device__ __forceinline__ int32_t rans_step(uint32_t& st, uint32_t& a, uint32_t& w, E& e,
+                                             const E* tab) {
+    const E cur = e;
     const uint32_t ns = entry_next_state(cur, st);
     const bool need = ns < kRansL;
     st = need ? ((ns << 16) | w) : ns;
@@ -403,10 +422,11 @@ template <int R>
 constexpr bool kEscapesInLds = R >= 32;
 
 // GROUP: a grouped launch (several matrices, slot found per workgroup);
-// otherwise slot 0 only, read at fixed kernel-argument offsets.
-template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP>
+// otherwise slot 0 only, read at fixed kernel-argument offsets.  T4: the
+// 4-byte table entries (the slot's table_lds then points at that image).
+template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP, bool T4>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs a) {
-    __shared__ __align__(16) TabEntry tab[kProbM];
+    __shared__ __align__(16) TabEntry<T4> tab[kProbM];
     __shared__ float red[kMaxWaves * R * B];
     __shared__ int flag[4];
     extern __shared__ __align__(16) uint16_t dyn[];
@@ -570,10 +590,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     };
 
     {
-        Lanes<S> L;
+        Lanes<S, TabEntry<T4>> L;
         uint32_t off0[S];
         stream_offsets<S>(len0, off0);
-        init_lanes<S>(L, tab, raw, st0, off0);
+        init_lanes(L, tab, raw, st0, off0);
         for (int k0 = 0; k0 < nk; k0 += KU) {
             convert();
             // unconditional: past the last block these read columns of the
@@ -763,7 +783,7 @@ __device__ __forceinline__ uint16_t to_bf16(float f) { return __builtin_bit_cast
 // tile (decoded as 0) with their side-table values, so no second launch.
 template <int R, int S, int MODE>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeArgs a) {
-    __shared__ __align__(16) TabEntry tab[kProbM];
+    __shared__ __align__(16) TabEntry<false> tab[kProbM];
     extern __shared__ __align__(16) uint16_t dyn[];
     constexpr int nst = 64 * S;
     constexpr int ESZ = MODE == 0 ? 4 : 2;
@@ -815,10 +835,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
     uint8_t* obase = static_cast<uint8_t*>(a.out) + (size_t)rb * R * a.cols * ESZ;
     const __amdgpu_buffer_rsrc_t ors =
         __builtin_amdgcn_make_buffer_rsrc(obase, 0, R * a.cols * ESZ, kBufWord3);
-    Lanes<S> L;
+    Lanes<S, TabEntry<false>> L;
     uint32_t off0[S];
     stream_offsets<S>(len0, off0);
-    init_lanes<S>(L, tab, raw, st0, off0);
+    init_lanes(L, tab, raw, st0, off0);
     // One block of nu <= KU column steps.  The loop below runs whole blocks
     // only (nu = KU, no early exit): exits after 1, 2 or 3 steps' stores
     // would meet at the loop latch, and the compiler would then wait there
@@ -932,8 +952,10 @@ bool fits_buffer_ranges(const rans_w64_matrix* m) {
 }
 
 bool valid_geometry(const rans_w64_matrix* m) {
-    if (!m || (m->flags & ~(RANS_F_WORDS_MASK | RANS_F_NO_ESCAPES)) ||
-        (m->flags & RANS_F_WORDS_MASK) == RANS_F_WORDS_MASK)
+    if (!m ||
+        (m->flags & ~(RANS_F_WORDS_MASK | RANS_F_NO_ESCAPES | RANS_F_TABLE4 | RANS_F_TABLE8)) ||
+        (m->flags & RANS_F_WORDS_MASK) == RANS_F_WORDS_MASK ||
+        ((m->flags & RANS_F_TABLE4) && (m->flags & RANS_F_TABLE8)))
         return false;
     if (m->rows <= 0 || m->cols <= 0 || m->R <= 0 || m->C <= 0 || m->S <= 0) return false;
     if (m->rows % m->R || m->cols % m->C || m->C % (64 * m->S)) return false;
@@ -985,71 +1007,132 @@ hipError_t ensure_lds(const void* fn, size_t bytes, int static_bytes) {
     return e;
 }
 
-template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP>
-int launch_gemv_t(const GemvArgs& a, int waves, size_t lds, int grid, hipStream_t stream) {
-    const void* fn =
-        reinterpret_cast<const void*>(&rans_w64_gemv_kernel<R, S, B, XBF16, REFILL, GROUP>);
-    hipError_t e = ensure_lds(fn, lds, gemv_static_lds(R));
-    if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((rans_w64_gemv_kernel<R, S, B, XBF16, REFILL, GROUP>), dim3(grid),
-                       dim3(64 * waves),
-                       lds, stream, a);
-    return (int)hipGetLastError();
+// The GEMV kernel for one launch: its address and its static LDS bytes
+// (nullptr when no instance is compiled).
+struct GemvFn {
+    const void* fn;
+    int static_lds;
+};
+
+template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP, bool T4>
+GemvFn gemv_fn_t() {
+    return {reinterpret_cast<const void*>(&rans_w64_gemv_kernel<R, S, B, XBF16, REFILL, GROUP, T4>),
+            gemv_static_lds(R, T4)};
 }
 
 // var: bit 0 = bf16 x, bit 1 = refill-only word fetch, bit 2 = grouped
-// launch (compiled for one state per lane only).
-template <int R, int S, int B, bool GROUP>
-int dispatch_xf(const GemvArgs& a, int var, int waves, size_t lds, int grid, hipStream_t st) {
+// launch, bit 3 = 4-byte table entries (bits 2 and 3 compiled for one state
+// per lane only, and not together).
+template <int R, int S, int B, bool GROUP, bool T4>
+GemvFn gemv_fn_xf(int var) {
     switch (var & 3) {
-        case 0: return launch_gemv_t<R, S, B, false, false, GROUP>(a, waves, lds, grid, st);
-        case 1: return launch_gemv_t<R, S, B, true, false, GROUP>(a, waves, lds, grid, st);
-        case 2: return launch_gemv_t<R, S, B, false, true, GROUP>(a, waves, lds, grid, st);
-        default: return launch_gemv_t<R, S, B, true, true, GROUP>(a, waves, lds, grid, st);
+        case 0: return gemv_fn_t<R, S, B, false, false, GROUP, T4>();
+        case 1: return gemv_fn_t<R, S, B, true, false, GROUP, T4>();
+        case 2: return gemv_fn_t<R, S, B, false, true, GROUP, T4>();
+        default: return gemv_fn_t<R, S, B, true, true, GROUP, T4>();
     }
 }
 
 template <int R, int S, int B>
-int dispatch_v(const GemvArgs& a, int var, int waves, size_t lds, int grid, hipStream_t st) {
-    if (var & 4) {
-        if constexpr (S == 1) return dispatch_xf<R, S, B, true>(a, var, waves, lds, grid, st);
-        return RANS_EUNSUPPORTED;
+GemvFn gemv_fn_v(int var) {
+    if (var & 12) {
+        if constexpr (S == 1) {
+            if ((var & 12) == 4) return gemv_fn_xf<R, S, B, true, false>(var);
+            if ((var & 12) == 8) return gemv_fn_xf<R, S, B, false, true>(var);
+        }
+        return {nullptr, 0};
     }
-    return dispatch_xf<R, S, B, false>(a, var, waves, lds, grid, st);
+    return gemv_fn_xf<R, S, B, false, false>(var);
 }
 
 template <int R, int S>
-int dispatch_b(const GemvArgs& a, int B, int var, int waves, size_t lds, int grid, hipStream_t st) {
+GemvFn gemv_fn_b(int B, int var) {
     switch (B) {
-        case 1: return dispatch_v<R, S, 1>(a, var, waves, lds, grid, st);
-        case 4: return dispatch_v<R, S, 4>(a, var, waves, lds, grid, st);
-        default: return RANS_EUNSUPPORTED;
+        case 1: return gemv_fn_v<R, S, 1>(var);
+        case 4: return gemv_fn_v<R, S, 4>(var);
+        default: return {nullptr, 0};
     }
 }
 
 template <int R>
-int dispatch_s(const GemvArgs& a, int S, int B, int var, int waves, size_t lds, int grid,
-               hipStream_t st) {
+GemvFn gemv_fn_s(int S, int B, int var) {
     switch (S) {
-        case 1: return dispatch_b<R, 1>(a, B, var, waves, lds, grid, st);
-        case 2: return dispatch_b<R, 2>(a, B, var, waves, lds, grid, st);
-        case 4: return dispatch_b<R, 4>(a, B, var, waves, lds, grid, st);
-        default: return RANS_EUNSUPPORTED;
+        case 1: return gemv_fn_b<R, 1>(B, var);
+        case 2: return gemv_fn_b<R, 2>(B, var);
+        case 4: return gemv_fn_b<R, 4>(B, var);
+        default: return {nullptr, 0};
     }
 }
 
-int dispatch_gemv(const GemvArgs& a, int R, int S, int B, int var, int waves, size_t lds, int grid,
-                  hipStream_t st) {
+GemvFn gemv_fn(int R, int S, int B, int var) {
     switch (R) {
-        case 1: return dispatch_s<1>(a, S, B, var, waves, lds, grid, st);
-        case 2: return dispatch_s<2>(a, S, B, var, waves, lds, grid, st);
-        case 3: return dispatch_s<3>(a, S, B, var, waves, lds, grid, st);
-        case 4: return dispatch_s<4>(a, S, B, var, waves, lds, grid, st);
-        case 8: return dispatch_s<8>(a, S, B, var, waves, lds, grid, st);
-        case 16: return dispatch_s<16>(a, S, B, var, waves, lds, grid, st);
-        case 35: return S == 1 ? dispatch_b<35, 1>(a, B, var, waves, lds, grid, st) : RANS_EUNSUPPORTED;
-        default: return RANS_EUNSUPPORTED;
+        case 1: return gemv_fn_s<1>(S, B, var);
+        case 2: return gemv_fn_s<2>(S, B, var);
+        case 3: return gemv_fn_s<3>(S, B, var);
+        case 4: return gemv_fn_s<4>(S, B, var);
+        case 8: return gemv_fn_s<8>(S, B, var);
+        case 16: return gemv_fn_s<16>(S, B, var);
+        case 35: return S == 1 ? gemv_fn_b<35, 1>(B, var) : GemvFn{nullptr, 0};
+        default: return {nullptr, 0};
     }
+}
+
+int launch_gemv_fn(GemvFn k, const GemvArgs& a, int waves, size_t lds, int grid,
+                   hipStream_t stream) {
+    if (!k.fn) return RANS_EUNSUPPORTED;
+    hipError_t e = ensure_lds(k.fn, lds, k.static_lds);
+    if (e != hipSuccess) return (int)e;
+    void* args[] = {const_cast<GemvArgs*>(&a)};
+    e = hipLaunchKernel(k.fn, dim3(grid), dim3(64 * waves), args, lds, stream);
+    const hipError_t last = hipGetLastError();
+    return (int)(e != hipSuccess ? e : last);
+}
+
+// Workgroups of kernel k that one CU holds at once with `lds` dynamic LDS
+// bytes, times the device's CUs (the runtime's occupancy query, which
+// counts registers, LDS and wave slots); cached per kernel and shape, since
+// launches repeat.  0 when the query fails.
+std::mutex g_occ_mu;
+struct OccEntry {
+    const void* fn;
+    int dev, waves;
+    size_t lds;
+    int64_t resident;
+};
+OccEntry g_occ[256];
+int g_occ_n = 0;
+
+int64_t resident_workgroups(GemvFn k, int waves, size_t lds) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lk(g_occ_mu);
+    for (int i = 0; i < g_occ_n; i++) {
+        const OccEntry& o = g_occ[i];
+        if (o.fn == k.fn && o.dev == dev && o.waves == waves && o.lds == lds) return o.resident;
+    }
+    int per_cu = 0, cus = 0;
+    if (ensure_lds(k.fn, lds, k.static_lds) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k.fn, 64 * waves, lds) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    const int64_t resident = (int64_t)per_cu * cus;
+    if (g_occ_n < 256) g_occ[g_occ_n++] = {k.fn, dev, waves, lds, resident};
+    return resident;
+}
+
+// Whether a single-matrix launch of the batch-B kernel runs with the 4-byte
+// table entries.  RANS_F_TABLE4 / RANS_F_TABLE8 decide when set.  Otherwise
+// only batch 1 with one state per lane does, and only when its grid is more
+// than the chip holds at once with the 8-byte entries: there the smaller
+// footprint lets more workgroups share a CU (and halves each random table
+// read's bytes), while a launch that is resident at once only pays the
+// longer decode step (+5% on 1536x8960), and the VALU-bound batch-4 kernel
+// the extra instructions (+11% on 25600x5120).
+bool use_table4(const rans_w64_matrix* m, int B, int var, int waves, size_t lds, int grid) {
+    if (m->flags & RANS_F_TABLE4) return true;
+    if ((m->flags & RANS_F_TABLE8) || B != 1 || m->S != 1) return false;
+    const int64_t resident = resident_workgroups(gemv_fn(m->R, m->S, B, var), waves, lds);
+    return resident > 0 && grid > resident;
 }
 
 // R = 35 (one state per lane only) splits rows of 8960 = 256 x 35 into 256
@@ -1188,7 +1271,14 @@ int launch_gemv_common(const rans_w64_matrix* const* ms, int n, const void* x, i
         a.x = static_cast<const uint8_t*>(x) + (size_t)done * m0->cols * xsz;
         for (int i = 0; i < n; i++) a.mat[i].y = ys[i] + (size_t)done * ms[i]->rows;
         a.nb = nb;
-        const int rc = dispatch_gemv(a, m0->R, m0->S, B, var, waves, lds, grid, stream);
+        int v = var;
+        if (n == 1 && (m0->flags & RANS_F_TABLE4 || m0->table_lds4) &&
+            use_table4(m0, B, var, waves, lds, grid))
+            v |= 8;
+        if (n == 1)
+            a.mat[0].table_lds =
+                reinterpret_cast<const uint4*>((v & 8) ? m0->table_lds4 : m0->table_lds);
+        const int rc = launch_gemv_fn(gemv_fn(m0->R, m0->S, B, v), a, waves, lds, grid, stream);
         if (rc != 0) return rc;
         done += nb;
     }
@@ -1201,6 +1291,10 @@ bool check_gemv_args(const rans_w64_matrix* m, const void* x, int x_dtype, int b
     if (!valid_pointers(m) || !x || !y || batch <= 0) return rc = RANS_EARG, false;
     if (x_dtype != RANS_X_F32 && x_dtype != RANS_X_BF16) return rc = RANS_EARG, false;
     if (!supported_rs(m->R, m->S)) return rc = RANS_EUNSUPPORTED, false;
+    if (m->flags & RANS_F_TABLE4) {
+        if (!m->table_lds4) return rc = RANS_EARG, false;
+        if (m->S != 1) return rc = RANS_EUNSUPPORTED, false;
+    }
     return true;
 }
 
@@ -1237,6 +1331,25 @@ extern "C" int launch_rans_gemv_group(const rans_w64_matrix* const* ms, int n, c
             return RANS_EGEOMETRY;
     }
     return launch_gemv_common(ms, n, x, x_dtype, batch, ys, stream);
+}
+
+extern "C" int rans_gemv_table4(const rans_w64_matrix* m, int x_dtype, int batch) {
+    if (!valid_geometry(m) || batch <= 0) return RANS_EGEOMETRY;
+    if (x_dtype != RANS_X_F32 && x_dtype != RANS_X_BF16) return RANS_EARG;
+    if (!supported_rs(m->R, m->S)) return RANS_EUNSUPPORTED;
+    if ((m->flags & RANS_F_TABLE4) && m->S != 1) return RANS_EUNSUPPORTED;
+    const int waves = gemv_waves(m);
+    if (!waves) return RANS_EGEOMETRY;
+    const int fetch = m->flags & RANS_F_WORDS_MASK;
+    const bool refill = fetch == RANS_F_WORDS_REFILL || (fetch == 0 && m->R >= 3);
+    const int var = (x_dtype == RANS_X_BF16 ? 1 : 0) | (refill ? 2 : 0);
+    const size_t lds = (size_t)waves * wave_layout(m).raw_words * 2;
+    const int grid = (m->rows / m->R) * ((m->cols / m->C) / waves);
+    // the batch-4 kernel runs chunks of 2 to 4 vectors, the batch-1 kernel a
+    // single remaining one (as launch_gemv_common splits a batch)
+    if (batch >= 2 && use_table4(m, 4, var, waves, lds, grid)) return 1;
+    if (batch % 4 == 1 && use_table4(m, 1, var, waves, lds, grid)) return 1;
+    return 0;
 }
 
 extern "C" int launch_rans_decode(const rans_w64_matrix* m, void* out_bf16, hipStream_t stream) {

@@ -118,6 +118,17 @@ extern "C" int rans_table_lds(const uint32_t* table, uint32_t* out) {
     return 0;
 }
 
+extern "C" int rans_table_lds4(const uint32_t* table, uint32_t* out) {
+    if (!table || !out) return RANS_EARG;
+    for (uint32_t i = 0; i < kM; i++) {
+        const uint32_t e = table[i];
+        const uint32_t sym = e & 0xFFu;
+        const uint32_t code = sym == 0 ? 0u : (uint32_t)((int32_t)sym - 128);
+        out[i] = ((e >> 8) & 0xFFFu) | ((e >> 20) << 12) | (code << 24);
+    }
+    return 0;
+}
+
 extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols, int32_t R,
                                int32_t C, int32_t S, int32_t nthreads, void** handle,
                                int64_t* info) {

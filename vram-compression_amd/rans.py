@@ -38,6 +38,7 @@ X_F32, X_BF16 = 0, 1
 # rans_w64_matrix.flags: word fetch of the GEMV (0 = library default), and
 # the empty-side-table promise (set by RansMatrix itself)
 F_WORDS_ALWAYS, F_WORDS_REFILL, F_WORDS_MASK, F_NO_ESCAPES = 1, 2, 3, 4
+F_TABLE8, F_TABLE4 = 8, 16
 # tile heights with compiled kernels; 35 only with one state per lane
 SUPPORTED_R = (35, 16, 8, 4, 3, 2, 1)
 
@@ -58,12 +59,14 @@ class RansMatrixDesc(ctypes.Structure):
                 ("esc_tileptr", ctypes.c_void_p),
                 ("esc_pos", ctypes.c_void_p), ("esc_val", ctypes.c_void_p),
                 ("step", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
-                ("workspace_bytes", ctypes.c_int64)]
+                ("workspace_bytes", ctypes.c_int64), ("table_lds4", ctypes.c_void_p)]
 
 
-EXPORTS = ("launch_rans_gemv", "rans_gemv_workspace_bytes", "launch_rans_gemv_group",
+EXPORTS = ("launch_rans_gemv", "rans_gemv_workspace_bytes", "rans_gemv_table4",
+           "launch_rans_gemv_group",
            "launch_rans_decode",
            "launch_rans_decode_codes", "launch_int4_gemv", "rans_build_table", "rans_table_lds",
+           "rans_table_lds4",
            "rans_w64_encode", "rans_w64_encode_fetch", "rans_w64_encode_counts",
            "rans_w64_encode_free",
            "rans_w64_decode_host")
@@ -94,6 +97,7 @@ def load_lib(path=LIB):
     sig = {
         "launch_rans_gemv": ([D, P, ctypes.c_int, ctypes.c_int, P, P], ctypes.c_int),
         "rans_gemv_workspace_bytes": ([D, ctypes.c_int], I64),
+        "rans_gemv_table4": ([D, ctypes.c_int, ctypes.c_int], ctypes.c_int),
         "launch_rans_gemv_group": ([P, ctypes.c_int, P, ctypes.c_int, ctypes.c_int, P, P],
                                    ctypes.c_int),
         "launch_rans_decode": ([D, P, P], ctypes.c_int),
@@ -101,6 +105,7 @@ def load_lib(path=LIB):
         "launch_int4_gemv": ([P, P, P, ctypes.c_int, ctypes.c_int, P], ctypes.c_int),
         "rans_build_table": ([P, I64, P, P, P], ctypes.c_int),
         "rans_table_lds": ([P, P], ctypes.c_int),
+        "rans_table_lds4": ([P, P], ctypes.c_int),
         "rans_w64_encode": ([P, I32, I32, I32, I32, I32, I32, ctypes.POINTER(P), P], ctypes.c_int),
         "rans_w64_encode_fetch": ([P] * 10, ctypes.c_int),
         "rans_w64_encode_counts": ([P, P], ctypes.c_int),
@@ -159,6 +164,17 @@ def table_lds(table, lib=None):
     out = np.zeros(2 * M, np.uint32)
     rc = (lib or _host_lib()).rans_table_lds(_p(t), _p(out))
     assert rc == 0, f"rans_table_lds failed ({rc})"
+    return out
+
+
+def table_lds4(table, lib=None):
+    """The 16 KB image of 4-byte LDS entries (uint32[4096]): per slot
+    freq | (slot - cum)<<12 | code<<24, code 0 for the escape symbol."""
+    t = np.ascontiguousarray(np.asarray(table, np.uint32).ravel())
+    assert t.size == M, "table must have 4096 slots"
+    out = np.zeros(M, np.uint32)
+    rc = (lib or _host_lib()).rans_table_lds4(_p(t), _p(out))
+    assert rc == 0, f"rans_table_lds4 failed ({rc})"
     return out
 
 
@@ -327,8 +343,11 @@ class RansMatrix:
 
     def __init__(self, enc, step, lib, flags=0):
         """flags: F_WORDS_ALWAYS / F_WORDS_REFILL picks the GEMV's word
-        fetch (same results, different speed); 0 lets the library choose.
-        F_NO_ESCAPES is added here when the matrix has no escapes."""
+        fetch and F_TABLE8 / F_TABLE4 its table entries (same results,
+        different speed); 0 lets the library choose.  F_NO_ESCAPES is added
+        here when the matrix has no escapes.  The 4-byte table image is
+        uploaded only where the library would use it (rans_gemv_table4 at
+        batch 1, bf16 x) or F_TABLE4 asks for it."""
         _require_gpu()
         if lib is None:
             raise RuntimeError("librans_hip.so not loaded")
@@ -362,7 +381,8 @@ class RansMatrix:
         self._desc = RansMatrixDesc(
             rows=self.rows, cols=self.cols, R=self.R, C=self.C, S=self.S,
             max_tile_words=self.max_tile_words, max_state_words=self.max_state_words,
-            flags=(int(flags) & F_WORDS_MASK) | (0 if len(enc["esc_pos"]) else F_NO_ESCAPES),
+            flags=(int(flags) & (F_WORDS_MASK | F_TABLE8 | F_TABLE4)) |
+            (0 if len(enc["esc_pos"]) else F_NO_ESCAPES),
             words=self.words.data_ptr(), tile_off=self.tile_off.data_ptr(),
             slen=self.slen.data_ptr(), states=self.states.data_ptr(),
             table=None, table_lds=self.table_lds.data_ptr(),
@@ -371,9 +391,16 @@ class RansMatrix:
             step=self.step.data_ptr(), workspace=None, workspace_bytes=0)
         self.workspace = None
         self._ensure_workspace(4)
-        # device bytes (the 32 KB table image in place of the 16 KB table)
+        self.table_lds4 = None
+        if flags & F_TABLE4 or (not flags & F_TABLE8 and
+                                lib.rans_gemv_table4(ctypes.byref(self._desc), X_BF16, 1) == 1):
+            self.table_lds4 = up(table_lds4(enc["table"], lib), np.int32)
+            self._desc.table_lds4 = self.table_lds4.data_ptr()
+        # device bytes (the 32 KB table image in place of the 16 KB table,
+        # plus the 16 KB image of 4-byte entries where it is used)
+        imgs = (self.table_lds,) if self.table_lds4 is None else (self.table_lds, self.table_lds4)
         self.nbytes = sum(t.numel() * t.element_size() for t in
-                          (self.words, self.tile_off, self.slen, self.states, self.table_lds,
+                          (self.words, self.tile_off, self.slen, self.states, *imgs,
                            self.esc_tileptr)) + 8 * int(len(enc["esc_pos"]))
 
     def tune(self, batch=1, x_dtype=torch.bfloat16, iters=20):
