@@ -482,3 +482,46 @@ def test_table_entries_choice(rans, lib, dev):
     assert m.table_lds4 is None
     for batch in (1, 4):
         assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, batch) == 0
+
+
+def test_table_choice_inside_graph_capture(rans, oracle, lib, dev):
+    """32768x256 in 1x256 tiles is 32768 one-wave workgroups, more than the
+    chip holds at once, so batch 1 runs on the 4-byte table entries.  The
+    library's first occupancy query for the f32-x kernel happens while a HIP
+    graph is being captured; every replay (with eager work between them)
+    equals the eager launch and the 8-byte entries, bit for bit."""
+    rows, cols = 32768, 256
+    print("case table choice under graph capture 32768x256", flush=True)
+    codes = oracle.synth_codes(rows, cols, 3.25, seed=21)
+    codes[100, 5] = -200
+    step = np.exp(0.5 * np.random.default_rng(4).standard_normal(cols)).astype(np.float32)
+    enc = rans.encode(codes, 1, 256, 1)
+    m = rans.RansMatrix(enc, torch.from_numpy(step), lib)
+    assert m.table_lds4 is not None
+    assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, 1) == 1
+    assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, 4) == 0
+    assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, 5) == 1
+    x = torch.randn(cols, device="cuda")
+    base = m._desc.flags & ~(rans.F_TABLE4 | rans.F_TABLE8)
+    # load both kernels outside the capture; forced choices skip the query
+    m._desc.flags = base | rans.F_TABLE8
+    y8 = m.gemv(x).clone()
+    m._desc.flags = base | rans.F_TABLE4
+    y4 = m.gemv(x).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(y8, y4)
+    ref = oracle.gemv_f64(codes, x.cpu().numpy().astype(np.float64), step.astype(np.float64))
+    assert _rel_l2(y4.cpu().numpy(), ref) <= REL_L2
+    m._desc.flags = base
+    y = torch.empty(rows, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        m.gemv(x, y)
+    for _ in range(3):
+        y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y8)
+        m.gemv(x * 2)  # eager work between replays
+        torch.cuda.synchronize()
+    assert torch.equal(m.gemv(x), y8)
