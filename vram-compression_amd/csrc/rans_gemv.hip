@@ -1091,7 +1091,9 @@ int launch_gemv_fn(GemvFn k, const GemvArgs& a, int waves, size_t lds, int grid,
 // Workgroups of kernel k that one CU holds at once with `lds` dynamic LDS
 // bytes, times the device's CUs (the runtime's occupancy query, which
 // counts registers, LDS and wave slots); cached per kernel and shape, since
-// launches repeat.  0 when the query fails.
+// launches repeat (the oldest entry is replaced once all 256 are in use).
+// 0 when the query fails.
+constexpr int kOccEntries = 256;
 std::mutex g_occ_mu;
 struct OccEntry {
     const void* fn;
@@ -1099,8 +1101,9 @@ struct OccEntry {
     size_t lds;
     int64_t resident;
 };
-OccEntry g_occ[256];
-int g_occ_n = 0;
+OccEntry g_occ[kOccEntries];
+int g_occ_n = 0;     // entries in use
+int g_occ_next = 0;  // the next to fill or replace
 
 int64_t resident_workgroups(GemvFn k, int waves, size_t lds) {
     int dev = 0;
@@ -1116,7 +1119,9 @@ int64_t resident_workgroups(GemvFn k, int waves, size_t lds) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return 0;
     const int64_t resident = (int64_t)per_cu * cus;
-    if (g_occ_n < 256) g_occ[g_occ_n++] = {k.fn, dev, waves, lds, resident};
+    g_occ[g_occ_next] = {k.fn, dev, waves, lds, resident};
+    g_occ_next = (g_occ_next + 1) % kOccEntries;
+    if (g_occ_n < kOccEntries) g_occ_n++;
     return resident;
 }
 
