@@ -30,8 +30,9 @@ Layout (all integers little endian, every section 64-byte aligned):
         esc_tileptr i32[ntiles+1], esc_pos i32[nesc], esc_val i32[nesc],
         step f32[cols]
 
-`flags` is the GEMV word-fetch policy chosen for the matrix (0 = library
-default), so a tuned set reloads with its tuning.
+`flags` holds the launch options chosen for the matrix (the RANS_F_* word
+fetch and table-entry bits; 0 = library defaults), so a tuned set reloads
+with its tuning.
 """
 import os
 import struct
