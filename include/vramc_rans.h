@@ -32,9 +32,10 @@
  *   - Symbol 0 is the escape: codes outside [-127, 127] are coded as symbol 0
  *     and their values live in a side table kept per tile: tile t's entries
  *     are esc_pos/esc_val[esc_tileptr[t] .. esc_tileptr[t+1]), esc_pos =
- *     (c << 8) | r for the code at tile row r, tile column c (row rb*R+r,
- *     column cb*C+c), strictly ascending within the tile, so a tile's
- *     entries run in column order (R <= 256).
+ *     c*R + r (16 bits) for the code at tile row r, tile column c (row
+ *     rb*R+r, column cb*C+c), strictly ascending within the tile, so a
+ *     tile's entries run in column order; esc_val is the code (16 bits).
+ *     Hence R*C <= 65536 and escape codes within [-32768, 32767].
  *   - words: all tile blocks concatenated; tile t's block is
  *     words[tile_off[t] .. tile_off[t+1]), a multiple of 8 words with at least
  *     one trailing pad word.  The streams of the tile's 64*S states follow
@@ -69,7 +70,8 @@ extern "C" {
 #define RANS_EGEOMETRY (-2)    /* shape not divisible, or tile too large for LDS */
 #define RANS_EWORKSPACE (-3)   /* split-K workspace missing or too small */
 #define RANS_EARG (-4)         /* null pointer or negative size */
-#define RANS_ECODES (-5)       /* encoder: degenerate or empty symbol distribution */
+#define RANS_ECODES (-5)       /* encoder: degenerate or empty symbol distribution, or a
+                                  code outside [-32768, 32767] */
 #define RANS_ETILE (-6)        /* encoder: a tile block exceeds 65535 words, or a state 255 */
 
 /* rans_w64_matrix.flags.  Word fetch (bits 0-1): how the GEMV fetches
@@ -104,8 +106,8 @@ typedef struct rans_w64_matrix {
     const uint32_t* table_lds;/* [8192], the table as the kernels hold it in LDS, made
                                  by rans_table_lds from table (device kernels) */
     const int32_t* esc_tileptr;/* [ntiles+1] */
-    const int32_t* esc_pos;   /* [nesc], (tile column << 8) | tile row */
-    const int32_t* esc_val;   /* [nesc] */
+    const uint16_t* esc_pos;  /* [nesc], tile column * R + tile row */
+    const int16_t* esc_val;   /* [nesc], the escaped codes */
     const float* step;        /* [cols] per-column step (waterfilling) */
     void* workspace;          /* split-K partials + counters; zero-filled once */
     int64_t workspace_bytes;
@@ -185,8 +187,9 @@ int rans_table_lds(const uint32_t* table, uint32_t* out);
 int rans_table_lds4(const uint32_t* table, uint32_t* out);
 
 /* Encode int32 codes (rows x cols, row-major) into the w64 format; replaces
- * encode() (rans.py:62-98).  R <= 256 and C < 2^23 (the side table's
- * position packing), else RANS_EGEOMETRY; RANS_ETILE when a tile block
+ * encode() (rans.py:62-98).  R*C <= 65536 (the side table's 16-bit
+ * positions), else RANS_EGEOMETRY; RANS_ECODES for a code outside
+ * [-32768, 32767] (the side table's 16-bit values); RANS_ETILE when a tile block
  * exceeds 65535 words or a state's stream 255 words.  On success *handle
  * owns the result and info[]
  * receives {nwords, ntiles, nstates, nesc, max_tile_words, payload_words,
@@ -197,7 +200,7 @@ int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols, int32_t R,
 
 int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off, uint8_t* slen,
                           uint32_t* states, uint32_t* table, int64_t* freq,
-                          int32_t* esc_tileptr, int32_t* esc_pos, int32_t* esc_val);
+                          int32_t* esc_tileptr, uint16_t* esc_pos, int16_t* esc_val);
 
 /* The symbol counts over the encoded matrix (256 x int64, symbol = code+128,
  * 0 for escapes), for the bit accounting.  No reference counterpart (the

@@ -284,15 +284,15 @@ def w64_decode(enc):
     codes = sym.astype(np.int64) - OFFSET
     esc_mask = sym == ESC
     # side table per tile: tile t owns entries tp[t]..tp[t+1], each at tile
-    # row pos & 255, tile column pos >> 8, strictly ascending within the tile
+    # row pos % R, tile column pos // R, strictly ascending within the tile
     tp = enc["esc_tileptr"].astype(np.int64)
     pos = enc["esc_pos"].astype(np.int64)
     eval_ = enc["esc_val"].astype(np.int64)
     if tp.size != ntiles + 1 or tp[0] != 0 or np.any(np.diff(tp) < 0) or tp[-1] != pos.size:
         raise AssertionError("escape tile pointers malformed")
     t = np.repeat(np.arange(ntiles), np.diff(tp))
-    r, c = pos & 0xFF, pos >> 8
-    if np.any(pos < 0) or np.any(r >= R) or np.any(c >= C):
+    r, c = pos % R, pos // R
+    if np.any(pos < 0) or np.any(c >= C):
         raise AssertionError("escape position outside its tile")
     same = t[1:] == t[:-1]
     if np.any(pos[1:][same] <= pos[:-1][same]):

@@ -69,8 +69,8 @@ def test_escapes_round_trip(rans, oracle):
     m = rng.random(codes.shape) < 0.01
     codes[m] = rng.integers(128, 600, m.sum()) * rng.choice([-1, 1], m.sum())
     codes[0, 0] = -128  # the reference alphabet's lowest code is an escape here
-    codes[5, 7] = 2 ** 30
-    codes[6, 8] = -(2 ** 31)
+    codes[5, 7] = 32767  # the 16-bit side table's extremes
+    codes[6, 8] = -32768
     R, C = 4, 128
     enc = rans.encode(codes, R, C, 1)
     esc = (codes < -127) | (codes > 127)
@@ -89,7 +89,7 @@ def test_escapes_round_trip(rans, oracle):
             for r in range(R):
                 v = codes[rb * R + r, cb * C + c]
                 if esc[rb * R + r, cb * C + c]:
-                    want_pos.append(c * 256 + r)
+                    want_pos.append(c * R + r)
                     want_val.append(v)
         np.testing.assert_array_equal(enc["esc_pos"][tp[t]:tp[t + 1]], want_pos)
         np.testing.assert_array_equal(enc["esc_val"][tp[t]:tp[t + 1]], want_val)
@@ -101,13 +101,13 @@ def test_escape_side_table_must_match_stream(rans, oracle):
     enc = rans.encode(codes, 4, 256, 1)
     codes[2, 9] = -300
     enc = rans.encode(codes, 4, 256, 1)
-    np.testing.assert_array_equal(enc["esc_pos"], [4 * 256 + 3, 9 * 256 + 2])
+    np.testing.assert_array_equal(enc["esc_pos"], [4 * 4 + 3, 9 * 4 + 2])  # c*R + r
     pos, val = enc["esc_pos"], enc["esc_val"]
-    for bad_pos, bad_val in [(pos + 256, val),                 # one column to the right
+    for bad_pos, bad_val in [(pos + 4, val),                   # one column to the right
                              (pos[::-1].copy(), val[::-1].copy()),  # not ascending
-                             (pos + 4, val),                   # tile rows 7 and 6 of 4
-                             (np.array([pos[0], pos[0]], np.int32), val)]:  # one entry twice
-        bad = dict(enc, esc_pos=bad_pos.astype(np.int32), esc_val=bad_val.astype(np.int32))
+                             (pos + 4 * 256, val),             # past the tile's last column
+                             (np.array([pos[0], pos[0]]), val)]:  # one entry twice
+        bad = dict(enc, esc_pos=bad_pos.astype(np.uint16), esc_val=bad_val.astype(np.int16))
         with pytest.raises(AssertionError):
             rans.decode_ref(bad)
         with pytest.raises(AssertionError):
@@ -155,10 +155,16 @@ def test_encode_rejects_bad_input(rans):
         rans.encode(ok, 4, 128, S=4)  # C % (64*S)
     with pytest.raises(AssertionError):
         rans.encode(np.zeros((0, 128), np.int32), 1, 128)
-    # a tile block beyond 65535 words
+    # a tile beyond 65536 codes (the side table's 16-bit positions)
     big = np.random.default_rng(1).integers(-127, 128, size=(16, 65536)).astype(np.int32)
-    with pytest.raises(AssertionError):
+    with pytest.raises(AssertionError, match="R\\*C"):
         rans.encode(big, 16, 65536)
+    # a code beyond the side table's 16-bit values
+    for v in (32768, -32769, 2 ** 30):
+        wide_code = ok.copy()
+        wide_code[3, 5] = v
+        with pytest.raises(AssertionError, match="32767"):
+            rans.encode(wide_code, 4, 128)
     # a state's stream beyond 255 words (1024 symbols of ~8 bits each), in
     # a tile block that itself fits
     wide = np.random.default_rng(2).integers(-127, 128, size=(16, 4096)).astype(np.int32)

@@ -93,8 +93,8 @@ struct MatArgs {
     const uint32_t* states;
     const uint4* table_lds;  // 2048 x 16 B LDS image of the table
     const int32_t* esc_tileptr;
-    const int32_t* esc_pos;
-    const int32_t* esc_val;
+    const uint16_t* esc_pos;  // tile-local index c*R + r
+    const int16_t* esc_val;
     const float* step;
     float* y;
     int rows, C, ncb;
@@ -125,8 +125,8 @@ struct DecodeArgs {
     const uint32_t* states;
     const uint4* table_lds;
     const int32_t* esc_tileptr;
-    const int32_t* esc_pos;
-    const int32_t* esc_val;
+    const uint16_t* esc_pos;  // tile-local index c*R + r
+    const int16_t* esc_val;
     const float* step;
     void* out;
     int rows, cols, C, ncb, ntiles;
@@ -393,6 +393,13 @@ __device__ __forceinline__ int32_t rans_step(uint32_t& st, uint32_t& a, uint32_t
     return entry_code(cur);
 }
 
+// Tile row and tile column of a side-table position c*R + r (R is a
+// compile-time constant, so the division is a multiply and shift).
+template <int R>
+__device__ __forceinline__ int esc_row(int pos) { return (int)((uint32_t)pos % (uint32_t)R); }
+template <int R>
+__device__ __forceinline__ uint32_t esc_tcol(int pos) { return (uint32_t)pos / (uint32_t)R; }
+
 // Adds an escape entry at tile row re to the lane's accumulators; v[b] is
 // value*step*x[b] (0 for a lane without an entry).  A 0/1 weight per row and
 // one FMA per (row, batch): 2R + RB instructions rather than R + 2RB for a
@@ -532,7 +539,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
     const int cbase = cb * m.C;
     // tile column of an entry, clamped into the tile so that no side-table
     // content can send a gather outside x or step
-    auto esc_col = [&](int pos) { return cbase + (int)min((uint32_t)pos >> 8, (uint32_t)(m.C - 1)); };
+    auto esc_col = [&](int pos) { return cbase + (int)min(esc_tcol<R>(pos), (uint32_t)(m.C - 1)); };
     int epos[P], eval[P];
 #pragma unroll
     for (int p = 0; p < P; p++) {
@@ -640,7 +647,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
                 const float ve = e < e_hi ? (float)eval[p] * __uint_as_float(esr[p]) : 0.f;
 #pragma unroll
                 for (int b = 0; b < B; b++) ev[b] = ve * bits_to_x(exr[p][b], XBF16);
-                add_escape<R, B>(acc, epos[p] & 0xFF, ev);
+                add_escape<R, B>(acc, esc_row<R>(epos[p]), ev);
             }
         }
         // further chunks (tiles with more than 64*P escapes)
@@ -653,7 +660,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
 #pragma unroll
             for (int b = 0; b < B; b++)
                 ev[b] = ve * load_x(a.x, (int64_t)min(b, a.nb - 1) * a.cols + col, XBF16);
-            add_escape<R, B>(acc, pos & 0xFF, ev);
+            add_escape<R, B>(acc, esc_row<R>(pos), ev);
         }
     }
 
@@ -691,7 +698,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
                 asm volatile("" : "+v"(esr[p]));
 #pragma unroll
                 for (int b = 0; b < B; b++) asm volatile("" : "+v"(exr[p][b]));
-                const int re = epos[p] & 0xFF;
+                const int re = esc_row<R>(epos[p]);
                 if (e < e_hi && re < R) {
                     const float ve = (float)eval[p] * __uint_as_float(esr[p]);
 #pragma unroll
@@ -705,7 +712,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
             const int e = e0 + lane;
             const int ec = min(e, e_hi - 1);
             const int pos = m.esc_pos[ec];
-            const int re = pos & 0xFF;
+            const int re = esc_row<R>(pos);
             const int col = esc_col(pos);
             const float ve = (float)m.esc_val[ec] * m.step[col];
             float xb[B];
@@ -895,8 +902,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
     const int cbase = cb * a.C;
     for (int e = e_lo + lane; e < e_hi; e += 64) {
         const int pos = a.esc_pos[e];
-        const int r = min(pos & 0xFF, R - 1);
-        const int col = cbase + (int)min((uint32_t)pos >> 8, (uint32_t)(a.C - 1));
+        const int r = esc_row<R>(pos);
+        const int col = cbase + (int)min(esc_tcol<R>(pos), (uint32_t)(a.C - 1));
         const int32_t v = a.esc_val[e];
         if (MODE == 0)
             __builtin_amdgcn_raw_buffer_store_b32(v, ors, (r * a.cols + col) * 4, 0, 0);

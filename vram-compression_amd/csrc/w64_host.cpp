@@ -30,7 +30,9 @@ struct Encoded {
     uint32_t table[kM];
     int64_t freq[256];
     int64_t counts[256] = {0};  // symbol counts over the matrix
-    std::vector<int32_t> esc_tileptr, esc_pos, esc_val;
+    std::vector<int32_t> esc_tileptr;
+    std::vector<uint16_t> esc_pos;  // tile-local index c*R + r
+    std::vector<int16_t> esc_val;
     int64_t payload_words = 0;
     int32_t max_tile_words = 0;
     int32_t max_state_words = 0;  // longest state stream, counting the tile padding
@@ -135,7 +137,7 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
     if (!codes || !handle || !info || rows <= 0 || cols <= 0 || R <= 0 || C <= 0 || S <= 0)
         return RANS_EARG;
     if (rows % R || cols % C || C % (64 * S)) return RANS_EGEOMETRY;
-    if (R > 256 || C >= (1 << 23)) return RANS_EGEOMETRY;  // esc_pos packing
+    if ((int64_t)R * C > 65536) return RANS_EGEOMETRY;  // 16-bit tile-local escape positions
     const int64_t N = (int64_t)rows * cols;
     auto* E = new Encoded();
 
@@ -146,6 +148,7 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
     const int nth = nthreads > 0 ? nthreads : 1;
     const int64_t nblk = std::min<int64_t>((int64_t)nth * 4, rows);
     std::vector<std::array<int64_t, 256>> hist((size_t)nblk);
+    std::vector<int> wide((size_t)nblk, 0);  // a code beyond the 16-bit escape values
     parallel_for(nblk, nth, [&](int64_t b) {
         std::array<int64_t, 256>& h = hist[(size_t)b];
         h.fill(0);
@@ -153,10 +156,16 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
         for (int64_t i = lo; i < hi; i++) {
             const int32_t v = codes[i];
             const uint8_t y = v >= -127 && v <= 127 ? (uint8_t)(v + 128) : (uint8_t)kEsc;
+            wide[(size_t)b] |= v < -32768 || v > 32767;
             sym[(size_t)i] = y;
             h[y]++;
         }
     });
+    for (int w : wide)
+        if (w) {
+            delete E;
+            return RANS_ECODES;
+        }
     for (const auto& h : hist)
         for (int y = 0; y < 256; y++) E->counts[y] += h[(size_t)y];
 
@@ -179,7 +188,8 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
     std::vector<int64_t> payload((size_t)ntiles, 0);
     std::vector<int> too_big((size_t)ntiles, 0);
     std::vector<int32_t> longest((size_t)ntiles, 0);
-    std::vector<std::vector<int32_t>> tesc_pos((size_t)ntiles), tesc_val((size_t)ntiles);
+    std::vector<std::vector<uint16_t>> tesc_pos((size_t)ntiles);
+    std::vector<std::vector<int16_t>> tesc_val((size_t)ntiles);
 
     const int64_t* freq = E->freq;
     parallel_for(ntiles, nthreads > 0 ? nthreads : 1, [&](int64_t t) {
@@ -237,8 +247,8 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
             for (int32_t r = 0; r < R; r++) {
                 const int64_t i = ((int64_t)rb * R + r) * cols + (int64_t)cb * C + c;
                 if (sym[(size_t)i] == kEsc) {
-                    tesc_pos[(size_t)t].push_back((c << 8) | r);
-                    tesc_val[(size_t)t].push_back(codes[i]);
+                    tesc_pos[(size_t)t].push_back((uint16_t)(c * R + r));
+                    tesc_val[(size_t)t].push_back((int16_t)codes[i]);
                 }
             }
     });
@@ -299,8 +309,8 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
 
 extern "C" int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off,
                                      uint8_t* slen, uint32_t* states, uint32_t* table,
-                                     int64_t* freq, int32_t* esc_tileptr, int32_t* esc_pos,
-                                     int32_t* esc_val) {
+                                     int64_t* freq, int32_t* esc_tileptr, uint16_t* esc_pos,
+                                     int16_t* esc_val) {
     if (!handle) return RANS_EARG;
     auto* E = static_cast<Encoded*>(handle);
     auto put = [](auto* dst, const auto& v) {
@@ -384,9 +394,8 @@ extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
         if (lo > hi || hi > nesc) return RANS_EARG;
         for (int32_t e = lo; e < hi; e++) {
             const int32_t pos = m->esc_pos[e];
-            const int32_t r = pos & 0xFF, c = pos >> 8;
-            if (pos < 0 || r >= R || c >= C || (e > lo && pos <= m->esc_pos[e - 1]))
-                return RANS_EARG;
+            const int32_t r = pos % R, c = pos / R;
+            if (c >= C || (e > lo && pos <= m->esc_pos[e - 1])) return RANS_EARG;
             int32_t* o = out + ((int64_t)rb * R + r) * cols + (int64_t)cb * C + c;
             if (*o != kEsc - 128) return RANS_EARG;
             *o = m->esc_val[e];

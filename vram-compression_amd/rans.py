@@ -190,8 +190,9 @@ def lane_order(sym, R, C, S=1):
 
 
 def encode(codes, R, C, S=1, threads=None):
-    """codes: integer array (rows x cols), any range; values outside
-    [-127, 127] go through the escape side table.  Returns a dict with the
+    """codes: integer array (rows x cols) within [-32768, 32767]; values
+    outside [-127, 127] go through the escape side table (16-bit tile-local
+    positions and 16-bit values, so R*C <= 65536).  Returns a dict with the
     w64 stream and the bit accounting of rans.py:95-97:
     bits_payload (renormalisation words), bits_state_offs (initial states,
     per-state offsets, tile offsets and tile padding), bits_table (16 KB
@@ -206,10 +207,10 @@ def encode(codes, R, C, S=1, threads=None):
     info = np.zeros(7, np.int64)
     nthreads = threads or min(16, os.cpu_count() or 1)
     rc = lib.rans_w64_encode(_p(codes), rows, cols, R, C, S, nthreads, ctypes.byref(h), _p(info))
-    assert rc != -5, "degenerate distribution (single symbol)"
+    assert rc != -5, "degenerate distribution (single symbol), or a code outside [-32768, 32767]"
     assert rc != -6, "a tile needs more than 65535 words, or a state more than 255: " \
                      "use smaller R or C"
-    assert rc != -2, "tile geometry outside the format (R <= 256, C < 2^23)"
+    assert rc != -2, "tile geometry outside the format (R*C <= 65536)"
     assert rc == 0, f"encode failed ({rc})"
     nwords, ntiles, nstates, nesc, max_tile_words, payload_words, max_state_words = \
         (int(v) for v in info)
@@ -220,8 +221,8 @@ def encode(codes, R, C, S=1, threads=None):
     table = np.zeros(M, np.uint32)
     freq = np.zeros(256, np.int64)
     esc_tileptr = np.zeros(ntiles + 1, np.int32)
-    esc_pos = np.zeros(nesc, np.int32)
-    esc_val = np.zeros(nesc, np.int32)
+    esc_pos = np.zeros(nesc, np.uint16)
+    esc_val = np.zeros(nesc, np.int16)
     counts = np.zeros(256, np.int64)
     try:
         rc = lib.rans_w64_encode_fetch(h, _p(words), _p(tile_off), _p(slen), _p(states),
@@ -243,7 +244,7 @@ def encode(codes, R, C, S=1, threads=None):
                 bits_payload=16 * payload_words / N,
                 bits_state_offs=(40 * nstates + 32 * (ntiles + 1) + 16 * pad_words) / N,
                 bits_table=32 * M / N,
-                bits_escape=32 * (ntiles + 1 + 2 * nesc) / N,
+                bits_escape=(32 * (ntiles + 1) + 32 * nesc) / N,
                 entropy_model=entropy_model)
 
 
@@ -371,8 +372,8 @@ class RansMatrix:
         self.table_lds = up(table_lds(enc["table"], lib), np.int32)
         self.esc_tileptr = up(enc["esc_tileptr"], np.int32)
         # never hand a zero-length buffer's (possibly null) pointer to the ABI
-        self.esc_pos = up(enc["esc_pos"] if len(enc["esc_pos"]) else np.zeros(1, np.int32), np.int32)
-        self.esc_val = up(enc["esc_val"] if len(enc["esc_val"]) else np.zeros(1, np.int32), np.int32)
+        self.esc_pos = up(enc["esc_pos"] if len(enc["esc_pos"]) else np.zeros(1, np.uint16), np.int16)
+        self.esc_val = up(enc["esc_val"] if len(enc["esc_val"]) else np.zeros(1, np.int16), np.int16)
         step = torch.as_tensor(step)
         assert step.numel() == self.cols, "step must have one value per column"
         self.step = step.float().reshape(self.cols).contiguous().to(dev)
@@ -401,7 +402,7 @@ class RansMatrix:
         imgs = (self.table_lds,) if self.table_lds4 is None else (self.table_lds, self.table_lds4)
         self.nbytes = sum(t.numel() * t.element_size() for t in
                           (self.words, self.tile_off, self.slen, self.states, *imgs,
-                           self.esc_tileptr)) + 8 * int(len(enc["esc_pos"]))
+                           self.esc_tileptr)) + 4 * int(len(enc["esc_pos"]))
 
     def tune(self, batch=1, x_dtype=torch.bfloat16, iters=20):
         """Time the two word-fetch policies of the GEMV on this matrix and

@@ -9,8 +9,9 @@ Layout (all integers little endian, every section 64-byte aligned):
 
     header, 64 bytes
         magic      8 bytes  b"VRAMCW64"
-        version    u32      3 (1 and 2 held a row-CSR side table or 16-bit
-                            stream offsets; they are not read)
+        version    u32      4 (1 to 3 held a row-CSR side table, 16-bit
+                            stream offsets or a 32-bit side table; they are
+                            not read)
         nmat       u32      number of matrices
         index_off  u64      byte offset of the index
         file_bytes u64      total file size (truncation check)
@@ -27,7 +28,7 @@ Layout (all integers little endian, every section 64-byte aligned):
     sections
         words u16[nwords], tile_off u32[ntiles+1], slen u8[nstates],
         states u32[nstates], table u32[4096] (reference packing),
-        esc_tileptr i32[ntiles+1], esc_pos i32[nesc], esc_val i32[nesc],
+        esc_tileptr i32[ntiles+1], esc_pos u16[nesc], esc_val i16[nesc],
         step f32[cols]
 
 `flags` holds the launch options chosen for the matrix (the RANS_F_* word
@@ -43,14 +44,14 @@ import numpy as np
 import rans
 
 MAGIC = b"VRAMCW64"
-VERSION = 3
+VERSION = 4
 _HEADER = struct.Struct("<8sIIQQ32x")
 _RECORD = struct.Struct("<64s8i5Qd9QI")
 RECORD_BYTES = 256
 ALIGN = 64
 _SECTIONS = (("words", np.uint16), ("tile_off", np.uint32), ("slen", np.uint8),
              ("states", np.uint32), ("table", np.uint32), ("esc_tileptr", np.int32),
-             ("esc_pos", np.int32), ("esc_val", np.int32), ("step", np.float32))
+             ("esc_pos", np.uint16), ("esc_val", np.int16), ("step", np.float32))
 assert _HEADER.size == 64 and _RECORD.size <= RECORD_BYTES
 
 
@@ -171,7 +172,7 @@ def load(path, verify=True, mmap=True):
                    bits_payload=16 * payload_words / N,
                    bits_state_offs=(40 * nstates + 32 * (ntiles + 1) + 16 * pad) / N,
                    bits_table=32 * rans.M / N,
-                   bits_escape=32 * (ntiles + 1 + 2 * nesc) / N,
+                   bits_escape=(32 * (ntiles + 1) + 32 * nesc) / N,
                    entropy_model=entropy_model)
         out.append(dict(name=name, enc=enc, step=arrays["step"], flags=flags))
     return out
