@@ -525,3 +525,30 @@ def test_table_choice_inside_graph_capture(rans, oracle, lib, dev):
         m.gemv(x * 2)  # eager work between replays
         torch.cuda.synchronize()
     assert torch.equal(m.gemv(x), y8)
+
+
+@pytest.mark.parametrize("R,C", [(3, 256), (16, 128), (35, 192)])
+def test_escape_value_extremes(rans, oracle, lib, dev, R, C):
+    """The side table's 16-bit values at their extremes (-32768, 32767, and
+    the smallest escapes -128 and 128) come back through the kernels'
+    sign-extending loads: int32 and bf16 decodes bit-exact, GEMV within the
+    bar, on the single-pass, split-K and LDS-escape (R = 35) paths."""
+    rows, cols = R * 8, C * (16 if R == 16 else 6)  # 16 column tiles: two column groups
+    print(f"case escape extremes R={R} C={C}", flush=True)
+    codes = oracle.synth_codes(rows, cols, 3.0, seed=R)
+    rng = np.random.default_rng(R)
+    for v in (-32768, 32767, -128, 128, -129, 4095):
+        for _ in range(3):
+            codes[rng.integers(rows), rng.integers(cols)] = v
+    step = np.exp(0.3 * rng.standard_normal(cols)).astype(np.float32)
+    enc = rans.encode(codes, R, C, 1)
+    assert enc["esc_val"].min() == -32768 and enc["esc_val"].max() == 32767
+    m = rans.RansMatrix(enc, torch.from_numpy(step), lib)
+    np.testing.assert_array_equal(m.decode_codes().cpu().numpy(), codes)
+    want = (torch.from_numpy(codes.astype(np.float32)) * torch.from_numpy(step)).bfloat16()
+    assert torch.equal(m.decode().cpu().view(torch.int16), want.view(torch.int16))
+    for batch in (1, 4):
+        x = torch.from_numpy(rng.standard_normal((batch, cols)).astype(np.float32)).cuda().bfloat16()
+        ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64),
+                              step.astype(np.float64))
+        assert _rel_l2(m.gemv(x).cpu().numpy(), ref) <= REL_L2
