@@ -484,6 +484,28 @@ def test_table_entries_choice(rans, lib, dev):
         assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, batch) == 0
 
 
+def test_two_tile_rows_per_workgroup(rans, oracle, lib, dev):
+    """1536x8960 in 3x2240 tiles (512 tile rows of 4 waves) runs two tile
+    rows per workgroup, 256 workgroups that share one table copy each.
+    Forcing the 4-byte table entries keeps one tile row per workgroup: the
+    two launches agree bit for bit (each row's sum runs over the same waves
+    in the same order), at batch 1, 4 and 5, escapes included."""
+    import rans_bench as B
+    print("case two tile rows per workgroup 1536x8960", flush=True)
+    codes = B.synth_codes_full(1536, 8960, 2.25, dist="laplace", seed=5, escape_frac=0.001)
+    step = torch.from_numpy(B.lognormal_steps(8960, seed=5))
+    enc = rans.encode(codes, 3, 2240, 1)
+    m2 = rans.RansMatrix(enc, step, lib)
+    m1 = rans.RansMatrix(enc, step, lib, flags=rans.F_TABLE4)
+    for batch in (1, 4, 5):
+        x = torch.randn(batch, 8960, device="cuda").bfloat16()
+        y2 = m2.gemv(x).cpu()
+        assert torch.equal(y2, m1.gemv(x).cpu()), batch
+        ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64),
+                              step.numpy().astype(np.float64))
+        assert _rel_l2(y2.numpy(), ref) <= REL_L2
+
+
 def test_table_choice_inside_graph_capture(rans, oracle, lib, dev):
     """32768x256 in 1x256 tiles is 32768 one-wave workgroups, more than the
     chip holds at once, so batch 1 runs on the 4-byte table entries.  The

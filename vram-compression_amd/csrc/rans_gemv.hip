@@ -27,6 +27,7 @@
 //      fixed order (no atomics on y, no memset, deterministic).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <mutex>
 #include <type_traits>
@@ -431,7 +432,10 @@ constexpr bool kEscapesInLds = R >= 32;
 // GROUP: a grouped launch (several matrices, slot found per workgroup);
 // otherwise slot 0 only, read at fixed kernel-argument offsets.  T4: the
 // 4-byte table entries (the slot's table_lds then points at that image).
-template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP, bool T4>
+// ROWS2: each workgroup takes two adjacent tile rows, W/2 waves each, so
+// one table copy serves twice the waves (single pass over the columns
+// only: no split-K).
+template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP, bool T4, bool ROWS2>
 __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs a) {
     __shared__ __align__(16) TabEntry<T4> tab[kProbM];
     __shared__ float red[kMaxWaves * R * B];
@@ -459,9 +463,13 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
                  "s"(m.esc_val), "s"(m.C), "s"(a.cols),
                  "s"(m.raw_words), "s"(a.W), "s"(m.ncb), "s"(a.ngroups), "s"(a.nb));
     const int bid = (int)blockIdx.x - (GROUP ? a.wg_begin[mi] : 0);
-    const int rb = bid / a.ngroups;
-    const int g = bid - rb * a.ngroups;
-    const int cb = g * W + wave;  // W divides ncb: every wave has a tile
+    constexpr int RPW = ROWS2 ? 2 : 1;  // tile rows per workgroup
+    const int Wt = ROWS2 ? W / 2 : W;   // waves per tile row
+    const int rsub = ROWS2 ? (wave >= Wt ? 1 : 0) : 0;
+    const int rb0 = (bid / a.ngroups) * RPW;
+    const int rb = rb0 + rsub;
+    const int g = bid - (bid / a.ngroups) * a.ngroups;
+    const int cb = g * Wt + (wave - rsub * Wt);  // Wt divides ncb: every wave has a tile
     const int t = rb * m.ncb + cb;
 
     // Everything the wave needs from memory before decoding is requested in
@@ -736,6 +744,18 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs 
         for (int ww = 0; ww < W; ww++) v += red[ww * NRB + i];
         return v;
     };
+    if constexpr (ROWS2) {
+        // each tile row summed over its own waves, in the same order as a
+        // one-row workgroup sums its W waves
+        for (int i = tid; i < RPW * NRB; i += nthr) {
+            const int rs = i / NRB, ii = i - rs * NRB;
+            float v = 0.f;
+            for (int ww = 0; ww < Wt; ww++) v += red[(rs * Wt + ww) * NRB + ii];
+            const int r = ii / B, b = ii - r * B;
+            if (b < a.nb) m.y[(int64_t)b * m.rows + (rb0 + rs) * R + r] = v;
+        }
+        return;
+    }
     if (a.ngroups == 1) {
         for (int i = tid; i < NRB; i += nthr) {
             const int r = i / B, b = i - r * B;
@@ -1021,35 +1041,39 @@ struct GemvFn {
     int static_lds;
 };
 
-template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP, bool T4>
+template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP, bool T4, bool ROWS2>
 GemvFn gemv_fn_t() {
-    return {reinterpret_cast<const void*>(&rans_w64_gemv_kernel<R, S, B, XBF16, REFILL, GROUP, T4>),
+    return {reinterpret_cast<const void*>(
+                &rans_w64_gemv_kernel<R, S, B, XBF16, REFILL, GROUP, T4, ROWS2>),
             gemv_static_lds(R, T4)};
 }
 
 // var: bit 0 = bf16 x, bit 1 = refill-only word fetch, bit 2 = grouped
-// launch, bit 3 = 4-byte table entries (bits 2 and 3 compiled for one state
-// per lane only, and not together).
-template <int R, int S, int B, bool GROUP, bool T4>
+// launch, bit 3 = 4-byte table entries, bit 4 = two tile rows per
+// workgroup (bits 2-4 compiled for one state per lane only, at most one of
+// them, and bit 4 not for 35-row tiles).
+template <int R, int S, int B, bool GROUP, bool T4, bool ROWS2>
 GemvFn gemv_fn_xf(int var) {
     switch (var & 3) {
-        case 0: return gemv_fn_t<R, S, B, false, false, GROUP, T4>();
-        case 1: return gemv_fn_t<R, S, B, true, false, GROUP, T4>();
-        case 2: return gemv_fn_t<R, S, B, false, true, GROUP, T4>();
-        default: return gemv_fn_t<R, S, B, true, true, GROUP, T4>();
+        case 0: return gemv_fn_t<R, S, B, false, false, GROUP, T4, ROWS2>();
+        case 1: return gemv_fn_t<R, S, B, true, false, GROUP, T4, ROWS2>();
+        case 2: return gemv_fn_t<R, S, B, false, true, GROUP, T4, ROWS2>();
+        default: return gemv_fn_t<R, S, B, true, true, GROUP, T4, ROWS2>();
     }
 }
 
 template <int R, int S, int B>
 GemvFn gemv_fn_v(int var) {
-    if (var & 12) {
+    if (var & 28) {
         if constexpr (S == 1) {
-            if ((var & 12) == 4) return gemv_fn_xf<R, S, B, true, false>(var);
-            if ((var & 12) == 8) return gemv_fn_xf<R, S, B, false, true>(var);
+            if ((var & 28) == 4) return gemv_fn_xf<R, S, B, true, false, false>(var);
+            if ((var & 28) == 8) return gemv_fn_xf<R, S, B, false, true, false>(var);
+            if constexpr (R != 35)
+                if ((var & 28) == 16) return gemv_fn_xf<R, S, B, false, false, true>(var);
         }
         return {nullptr, 0};
     }
-    return gemv_fn_xf<R, S, B, false, false>(var);
+    return gemv_fn_xf<R, S, B, false, false, false>(var);
 }
 
 template <int R, int S>
@@ -1130,6 +1154,39 @@ int64_t resident_workgroups(GemvFn k, int waves, size_t lds) {
     g_occ_next = (g_occ_next + 1) % kOccEntries;
     if (g_occ_n < kOccEntries) g_occ_n++;
     return resident;
+}
+
+// CUs of the current device, cached per device; 0 when the query fails.
+std::atomic<int> g_cus[64];
+
+int device_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64) {
+        const int v = g_cus[dev].load(std::memory_order_relaxed);
+        if (v > 0) return v;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    if (dev < 64) g_cus[dev].store(cus, std::memory_order_relaxed);
+    return cus;
+}
+
+// Whether a launch takes two tile rows per workgroup.  The 32 KB table copy
+// of each workgroup sits on the critical path of a launch the chip holds at
+// once (copying it twice made 1536x8960 6% slower); two rows per workgroup
+// halve the copies (1536x8960: 1.3-2.8% faster over two boxes, 1536x8960 at
+// 2.25 bits with escapes 5%).  Only while the halved grid still gives
+// every CU a workgroup: 1536x1536 in 8x384 tiles (192 workgroups) ran 3-5%
+// slower as 96.  Single-matrix launches with one state per lane, one
+// workgroup per tile row (no split-K), at most 4 waves per row, an even
+// number of tile rows and the 8-byte table entries; not 35-row tiles.
+bool use_rows2(const rans_w64_matrix* m, int n, int v, int waves, int ngroups, int grid) {
+    if (n != 1 || m->S != 1 || (v & 8) || m->R == 35 || ngroups != 1) return false;
+    if (2 * waves > kMaxWaves || (m->rows / m->R) % 2) return false;
+    const int cus = device_cus();
+    return cus > 0 && grid >= 2 * cus;
 }
 
 // Whether a single-matrix launch of the batch-B kernel runs with the 4-byte
@@ -1290,7 +1347,11 @@ int launch_gemv_common(const rans_w64_matrix* const* ms, int n, const void* x, i
         if (n == 1)
             a.mat[0].table_lds =
                 reinterpret_cast<const uint4*>((v & 8) ? m0->table_lds4 : m0->table_lds);
-        const int rc = launch_gemv_fn(gemv_fn(m0->R, m0->S, B, v), a, waves, lds, grid, stream);
+        const bool rows2 = use_rows2(m0, n, v, waves, ngroups, grid);
+        if (rows2) v |= 16;
+        a.W = rows2 ? 2 * waves : waves;
+        const int rc = launch_gemv_fn(gemv_fn(m0->R, m0->S, B, v), a, a.W, rows2 ? 2 * lds : lds,
+                                      rows2 ? grid / 2 : grid, stream);
         if (rc != 0) return rc;
         done += nb;
     }
