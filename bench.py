@@ -47,7 +47,7 @@ DEFAULT_TILING = (3, 2240, 1)
 # is scaled by what it reads for an elementwise kernel that reads and writes
 # 256 MiB: reads x2.0, writes x1.0.  Commands and counts:
 # profiles/rans_w64_gemv_1536x8960_3.25b.md.  Keyed by (R, C, S, word fetch).
-PMC_TRAFFIC_KIB = {(3, 2240, 1, "refill"): (3486.9, 20.0)}
+PMC_TRAFFIC_KIB = {(3, 2240, 1, "refill"): (3445.6, 12.0)}
 PMC_FETCH_FACTOR, PMC_WRITE_FACTOR = 2.0, 1.0
 
 
