@@ -574,3 +574,27 @@ def test_escape_value_extremes(rans, oracle, lib, dev, R, C):
         ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64),
                               step.astype(np.float64))
         assert _rel_l2(m.gemv(x).cpu().numpy(), ref) <= REL_L2
+
+
+@pytest.mark.parametrize("tile_rows", [513, 514])
+def test_two_tile_rows_odd_and_even(rans, oracle, lib, dev, tile_rows):
+    """A grid of at least twice the CUs pairs tile rows only when their
+    count is even: 513 tile rows of 3x2240 tiles keep one row per
+    workgroup, 514 pair them.  Both agree with the one-row launch (forced
+    through the 4-byte table entries) bit for bit, and with the oracle."""
+    import rans_bench as B
+    rows, cols = 3 * tile_rows, 8960
+    print(f"case tile rows {tile_rows}", flush=True)
+    codes = B.synth_codes_full(rows, cols, 3.25, dist="laplace", seed=tile_rows)
+    codes[rows - 1, cols - 1] = 900  # an escape in the last tile row
+    step = torch.from_numpy(B.lognormal_steps(cols, seed=tile_rows))
+    enc = rans.encode(codes, 3, 2240, 1)
+    m = rans.RansMatrix(enc, step, lib)
+    m1 = rans.RansMatrix(enc, step, lib, flags=rans.F_TABLE4)
+    for batch in (1, 4):
+        x = torch.randn(batch, cols, device="cuda").bfloat16()
+        y = m.gemv(x).cpu()
+        assert torch.equal(y, m1.gemv(x).cpu())
+        ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64),
+                              step.numpy().astype(np.float64))
+        assert _rel_l2(y.numpy(), ref) <= REL_L2
