@@ -10,10 +10,13 @@ x ~ N(0,1) in bf16; batch 1.  A step is one GEMV y = codes @ (x*step).
 
 Timing: W warm-up launches, then K launches captured in one HIP graph (so
 Python dispatch cost is not measured) and replayed between HIP events on the
-launch stream.  Successive launches rotate over enough distinct encoded
-copies (>= 512 MB) that the 256 MB Infinity Cache and the L2 cannot serve the
-compressed stream; a hot-cache figure (one copy) is reported separately, as
-is torch's bf16 F.linear (rocBLAS/hipBLASLt) on the same shape and rotation.
+launch stream.  Launches rotate over distinct encoded copies so that every
+timed launch reads a copy that >= 512 MiB of other copies have passed through
+the caches since its last read: the 256 MB Infinity Cache and the L2 cannot
+serve the compressed stream, whatever K is (with K below the copies 512 MiB
+take, an untimed replay over the other copies runs just before the timed
+one).  A hot-cache figure (one copy) is reported separately, as is torch's
+bf16 F.linear (rocBLAS/hipBLASLt) on the same shape and rotation.
 
 Prints one JSON line.  `value` is the bf16-equivalent effective weight
 throughput rows*cols*2 bytes / time per GEMV.
@@ -62,10 +65,30 @@ def algorithmic_bytes(enc, rows, cols, batch=1):
     return comp, comp + cols * 2 * batch + cols * 4 + rows * 4 * batch
 
 
-def graph_time_us(fns, steps, warmup):
-    """Device microseconds per call of K=steps calls captured in one graph."""
+def copies_for(steps, nbytes):
+    """Distinct copies of an nbytes operand for a rotated run of `steps`
+    launches: n512 = ceil(512 MiB / nbytes) copies when steps >= n512 (the
+    timed launches cycle through them, so every copy is read again only
+    after >= 512 MiB of other copies), else steps + n512 (the timed launches
+    use the first `steps`, an untimed flush replay reads the other n512
+    just before them)."""
+    n512 = max(2, -(-ROTATE_BYTES // nbytes))
+    return n512 if steps >= n512 else steps + n512
+
+
+def graph_time_us(fns, steps, warmup, rotate=None):
+    """Device microseconds per call of exactly `steps` calls captured in one
+    HIP graph and replayed between HIP events on the launch stream.
+
+    rotate (the number of copies the calls in fns rotate over, len(fns)):
+    when steps is smaller than that, the timed graph runs calls 0..steps-1
+    and a second, untimed graph runs all the others just before the timed
+    replay, so every timed call reads a copy that at least 512 MiB of other
+    copies have displaced from the 256 MB Infinity Cache and the L2 since
+    its last read; otherwise the timed calls cycle through all copies."""
+    n = len(fns)
     for i in range(warmup):
-        fns[i % len(fns)]()
+        fns[i % n]()
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -76,8 +99,16 @@ def graph_time_us(fns, steps, warmup):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for i in range(steps):
-            fns[i % len(fns)]()
+            fns[i % n]()
+    flush = None
+    if rotate and steps < n:
+        flush = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(flush):
+            for i in range(steps, n):
+                fns[i]()
     g.replay()  # untimed: first replay uploads the graph
+    if flush is not None:
+        flush.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -85,6 +116,15 @@ def graph_time_us(fns, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1000.0 / steps
+
+
+def rotation_record(steps, ncopy, nbytes):
+    """What a rotated measurement read: copies, bytes, and the least data
+    read between two reads of one copy."""
+    cycle = ncopy if steps >= ncopy else ncopy - steps
+    return {"copies": ncopy, "bytes": ncopy * nbytes, "timed_launches": steps,
+            "copies_read_in_timed_region": min(steps, ncopy),
+            "bytes_between_reads_of_a_copy": cycle * nbytes}
 
 
 def cpu_baseline(codes, step, x, budget_s=12.0):
@@ -223,13 +263,13 @@ def main():
     def measure(R, C, S, steps):
         enc = rans.encode(codes, R, C, S)
         comp, alg = algorithmic_bytes(enc, ROWS, COLS)
-        ncopy = max(2, -(-ROTATE_BYTES // comp))
+        ncopy = copies_for(steps, comp)
         m0 = rans.RansMatrix(enc, step_t, lib)
         flags = pick_fetch(m0)
         ms = [m0] + [rans.RansMatrix(enc, step_t, lib, flags=flags) for _ in range(ncopy - 1)]
         y = torch.empty(ROWS, device="cuda")
         fns = [lambda m=m: m.gemv(xb, y) for m in ms]
-        t_rot = graph_time_us(fns, steps, args.warmup)
+        t_rot = graph_time_us(fns, steps, args.warmup, rotate=ncopy)
         t_hot = graph_time_us(fns[:1], steps, args.warmup)
         del ms, m0
         torch.cuda.empty_cache()
@@ -284,24 +324,25 @@ def main():
     rocblas = None
     if not args.no_rocblas:
         W = (torch.from_numpy(codes.astype(np.float32)) * step_t).bfloat16()
-        nW = max(2, -(-ROTATE_BYTES // (ROWS * COLS * 2)))
+        nW = copies_for(args.steps, ROWS * COLS * 2)
         Ws = [W.cuda() for _ in range(nW)]
         fns = [lambda Wd=Wd: torch.nn.functional.linear(xb, Wd) for Wd in Ws]
-        tb_rot = graph_time_us(fns, args.steps, args.warmup)
+        tb_rot = graph_time_us(fns, args.steps, args.warmup, rotate=nW)
         tb_hot = graph_time_us(fns[:1], args.steps, args.warmup)
         rocblas = {"us_per_gemv": tb_rot, "effective_GBps": ROWS * COLS * 2 / tb_rot / 1e3,
                    "hot_us_per_gemv": tb_hot, "copies": nW,
+                   "rotation": rotation_record(args.steps, nW, ROWS * COLS * 2),
                    "speedup_rans_vs_bf16": tb_rot / t_rot}
         del Ws, fns
         # the reference's other comparators (kernel/bench.py:97-111): the
         # fixed-rate int4 GEMV (host fold + int4 kernel) and decode-to-bf16
         # followed by the bf16 GEMV
-        m4s = [rans.Int4Matrix(np.clip(codes, -8, 7), step_t, lib)
-               for _ in range(max(2, -(-ROTATE_BYTES // (ROWS * COLS // 2))))]
+        n4 = copies_for(args.steps, ROWS * COLS // 2)
+        m4s = [rans.Int4Matrix(np.clip(codes, -8, 7), step_t, lib) for _ in range(n4)]
         xf = xb.float()
         y4 = torch.empty(ROWS, device="cuda")
         rocblas["int4_us_per_gemv"] = graph_time_us([lambda m4=m4: m4.gemv(xf, y4) for m4 in m4s],
-                                                    args.steps, args.warmup)
+                                                    args.steps, args.warmup, rotate=n4)
         del m4s
         m = rans.RansMatrix(enc, step_t, lib)
         buf = torch.empty(ROWS, COLS, device="cuda", dtype=torch.bfloat16)
@@ -349,6 +390,7 @@ def main():
                    "rows": ROWS, "cols": COLS, "batch": 1, "R": R, "C": C, "S": S,
                    "states": int(len(enc["states"])), "bits_total": bits_total,
                    "bits_payload": enc["bits_payload"], "rotating_copies": ncopy,
+                   "rotation": rotation_record(args.steps, ncopy, comp),
                    "word_fetch": {1: "always", 2: "refill"}.get(measure.flags & 3, "default"),
                    "parallelism": "single GPU"},
         "us_per_gemv": t_rot,

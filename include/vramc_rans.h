@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-/* x dtype codes for launch_rans_gemv */
+/* x dtype codes for rans_w64_gemv */
 #define RANS_X_F32 0
 #define RANS_X_BF16 1
 
@@ -122,10 +122,10 @@ typedef struct rans_w64_matrix {
  * f32, written (never accumulated into).  The per-column step is folded into
  * x inside the kernel.  Replaces launch_rans_gemv (rans_gemv.cu:146-153),
  * which takes a host-folded f32 x and needs y zeroed when cols != C. */
-int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
-                     void* y, hipStream_t stream);
+int rans_w64_gemv(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
+                  void* y, hipStream_t stream);
 
-/* 1 when launch_rans_gemv at this batch and x dtype would run any of its
+/* 1 when rans_w64_gemv at this batch and x dtype would run any of its
  * launches with the 4-byte table entries, were table_lds4 set (0 if not, or
  * a negative RANS_E* for arguments it would reject).  A caller asks before
  * building the 16 KB image, which only such matrices need.  Uses the
@@ -133,12 +133,19 @@ int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_dtype, int b
  * counterpart. */
 int rans_gemv_table4(const rans_w64_matrix* m, int x_dtype, int batch);
 
-/* Bytes of workspace launch_rans_gemv needs for this matrix and batch (0 when
+/* Bytes of workspace rans_w64_gemv needs for this matrix and batch (0 when
  * one workgroup covers a whole tile row).  The first 4096 bytes are counters
  * that must be zero before the first launch; the kernel leaves them zero. */
 int64_t rans_gemv_workspace_bytes(const rans_w64_matrix* m, int batch);
 
-/* launch_rans_gemv for n <= 4 matrices that share x, in one launch:
+/* 1 when a single-matrix rans_w64_gemv launch at this batch and x dtype would
+ * take two tile rows per workgroup (one staged table serving both rows'
+ * waves), 0 if not, or a negative RANS_E* for arguments it would reject.
+ * Uses the current device's CU count; launches nothing.  No reference
+ * counterpart. */
+int rans_gemv_rows2(const rans_w64_matrix* m, int x_dtype, int batch);
+
+/* rans_w64_gemv for n <= 4 matrices that share x, in one launch:
  * ys[i] (batch x ms[i]->rows f32) gets ms[i]'s product.  No reference
  * counterpart: it is for projections that read the same activations (a
  * layer's q, k and v, or its gate and up), whose separate GEMVs each leave
@@ -146,24 +153,38 @@ int64_t rans_gemv_workspace_bytes(const rans_w64_matrix* m, int batch);
  * and one workgroup per tile row (cols/C equal to the waves per workgroup,
  * the same for all: cols/C <= 8 and the tile block within LDS); otherwise
  * RANS_EUNSUPPORTED (or RANS_EGEOMETRY) and nothing is launched.  Results
- * are bitwise those of separate launch_rans_gemv calls. */
-int launch_rans_gemv_group(const rans_w64_matrix* const* ms, int n, const void* x, int x_dtype,
-                           int batch, float* const* ys, hipStream_t stream);
+ * are bitwise those of separate rans_w64_gemv calls. */
+int rans_w64_gemv_group(const rans_w64_matrix* const* ms, int n, const void* x, int x_dtype,
+                        int batch, float* const* ys, hipStream_t stream);
 
 /* Decode to a dense bf16 matrix out[r,c] = bf16(code[r,c]*step[c]) (round to
  * nearest even).  Replaces launch_rans_decode (rans_gemv.cu:155-162). */
-int launch_rans_decode(const rans_w64_matrix* m, void* out_bf16, hipStream_t stream);
+int rans_w64_decode(const rans_w64_matrix* m, void* out_bf16, hipStream_t stream);
 
 /* Decode to dense int32 codes out[r,c] = code[r,c], escapes included: the
  * bit-exact check path.  No reference counterpart (the reference compares
  * the bf16 decode, bench.py:49-51). */
-int launch_rans_decode_codes(const rans_w64_matrix* m, int32_t* out, hipStream_t stream);
+int rans_w64_decode_codes(const rans_w64_matrix* m, int32_t* out, hipStream_t stream);
 
 /* Fixed-rate 4-bit baseline GEMV, same contract as the reference
  * (rans_gemv.cu:164-170): w packs 8 codes per u32 (nibble b of word j of row
  * r is column 8j+b, value nibble-8), x is the host-folded f32 x*step, y f32. */
 int launch_int4_gemv(const void* w, const void* x, void* y, int rows, int cols,
                      hipStream_t stream);
+
+/* The reference's two rANS entry points, with its argument lists
+ * (rans_gemv.cu:146-162, bound by kernel/rans.py:25-29 as
+ * [c_int] + [c_void_p]*5 + [c_int]*3 + [c_void_p]).  They take the
+ * reference's 32-lane stream (words, offs), which this library does not
+ * decode on the GPU: both return RANS_EUNSUPPORTED and launch nothing, so a
+ * binding written for the reference gets the reference's own "unsupported"
+ * code instead of a crash.  The w64 format is launched with rans_w64_gemv and
+ * rans_w64_decode. */
+int launch_rans_gemv(int R, const void* words, const void* offs, const void* table,
+                     const void* x, void* y, int rows, int cols, int C, hipStream_t stream);
+int launch_rans_decode(int R, const void* words, const void* offs, const void* table,
+                       const void* step, void* out_bf16, int rows, int cols, int C,
+                       hipStream_t stream);
 
 /* ------------------------------------------------------------------ host */
 

@@ -263,7 +263,9 @@ def w64_decode(enc):
     Raises AssertionError on a stream that does not end in state 2^16."""
     lib = load()
     rows, cols = enc["shape"]
-    R, C, S = enc["R"], enc["C"], enc["S"]
+    # the w64 tiling (tile_R, tile_C); R and C of the dict are the tiling the
+    # encoder was asked for, which it may have mapped to another tile
+    R, C, S = enc.get("tile_R", enc["R"]), enc.get("tile_C", enc["C"]), enc["S"]
     tile_off = enc["tile_off"].astype(np.int64)
     ntiles = (rows // R) * (cols // C)
     nst = 64 * S

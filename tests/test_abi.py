@@ -19,7 +19,7 @@ def _declared():
 
 def test_header_declares_entry_points():
     names = _declared()
-    assert "launch_rans_gemv" in names and "launch_int4_gemv" in names
+    assert "rans_w64_gemv" in names and "launch_int4_gemv" in names
     assert len(names) == len(set(names))
 
 
@@ -42,16 +42,16 @@ def _desc(rans, rows=256, cols=4096, R=8, C=256, S=1, mtw=1024):
 def test_argument_validation_without_gpu(rans, lib):
     d = _desc(rans)
     x = y = ctypes.c_void_p(0x2000)
-    assert lib.launch_rans_gemv(None, x, 0, 1, y, None) == -2
+    assert lib.rans_w64_gemv(None, x, 0, 1, y, None) == -2
     bad = _desc(rans, cols=4000)
-    assert lib.launch_rans_gemv(ctypes.byref(bad), x, 0, 1, y, None) == -2
+    assert lib.rans_w64_gemv(ctypes.byref(bad), x, 0, 1, y, None) == -2
     r5 = _desc(rans, rows=255, R=5)  # no kernel compiled for R=5
-    assert lib.launch_rans_gemv(ctypes.byref(r5), x, 0, 1, y, None) == -1
-    assert lib.launch_rans_gemv(ctypes.byref(d), x, 7, 1, y, None) == -4
-    assert lib.launch_rans_gemv(ctypes.byref(d), None, 0, 1, y, None) == -4
-    assert lib.launch_rans_gemv(ctypes.byref(d), x, 0, 0, y, None) == -4
+    assert lib.rans_w64_gemv(ctypes.byref(r5), x, 0, 1, y, None) == -1
+    assert lib.rans_w64_gemv(ctypes.byref(d), x, 7, 1, y, None) == -4
+    assert lib.rans_w64_gemv(ctypes.byref(d), None, 0, 1, y, None) == -4
+    assert lib.rans_w64_gemv(ctypes.byref(d), x, 0, 0, y, None) == -4
     # 16 column tiles: 8 waves per workgroup, 2 column groups -> split-K workspace
-    assert lib.launch_rans_gemv(ctypes.byref(d), x, 0, 1, y, None) == -3
+    assert lib.rans_w64_gemv(ctypes.byref(d), x, 0, 1, y, None) == -3
     need = lib.rans_gemv_workspace_bytes(ctypes.byref(d), 1)
     assert need == 256 + 2 * 1 * 256 * 4
     assert lib.rans_gemv_workspace_bytes(ctypes.byref(d), 4) == 256 + 2 * 4 * 256 * 4
@@ -62,16 +62,16 @@ def test_argument_validation_without_gpu(rans, lib):
     for flags in (3, 24, 32, -1):  # both word-fetch bits, both table bits, an unknown bit
         bad_flags = _desc(rans, cols=2048)
         bad_flags.flags = flags
-        assert lib.launch_rans_gemv(ctypes.byref(bad_flags), x, 0, 1, y, None) == -2
+        assert lib.rans_w64_gemv(ctypes.byref(bad_flags), x, 0, 1, y, None) == -2
         assert lib.rans_gemv_table4(ctypes.byref(bad_flags), 0, 1) == -2
     # the 4-byte table entries, forced: they need their image and one state per lane
     t4 = _desc(rans, cols=2048)
     t4.flags = rans.F_TABLE4
-    assert lib.launch_rans_gemv(ctypes.byref(t4), x, 0, 1, y, None) == -4
+    assert lib.rans_w64_gemv(ctypes.byref(t4), x, 0, 1, y, None) == -4
     t4s2 = _desc(rans, cols=2048, S=2)
     t4s2.flags = rans.F_TABLE4
     t4s2.table_lds4 = 0x1000
-    assert lib.launch_rans_gemv(ctypes.byref(t4s2), x, 0, 1, y, None) == -1
+    assert lib.rans_w64_gemv(ctypes.byref(t4s2), x, 0, 1, y, None) == -1
     assert lib.rans_gemv_table4(ctypes.byref(t4s2), 0, 1) == -1
     # forced choices are answered without the occupancy query
     t4.table_lds4 = 0x1000
@@ -84,17 +84,17 @@ def test_argument_validation_without_gpu(rans, lib):
     assert lib.rans_table_lds4(None, y) == -4
     no_img = _desc(rans)
     no_img.table_lds = None  # the kernels need the table's LDS image
-    assert lib.launch_rans_gemv(ctypes.byref(no_img), x, 0, 1, y, None) == -4
-    assert lib.launch_rans_decode_codes(ctypes.byref(no_img), y, None) == -4
+    assert lib.rans_w64_gemv(ctypes.byref(no_img), x, 0, 1, y, None) == -4
+    assert lib.rans_w64_decode_codes(ctypes.byref(no_img), y, None) == -4
     assert lib.rans_table_lds(None, y) == -4
-    assert lib.launch_rans_decode(None, y, None) == -2
-    assert lib.launch_rans_decode_codes(ctypes.byref(d), None, None) == -4
+    assert lib.rans_w64_decode(None, y, None) == -2
+    assert lib.rans_w64_decode_codes(ctypes.byref(d), None, None) == -4
     assert lib.launch_int4_gemv(None, x, y, 4, 64, None) == -4
     assert lib.launch_int4_gemv(x, x, y, 4, 48, None) == -2
 
 
 def test_group_validation_without_gpu(rans, lib):
-    """launch_rans_gemv_group refuses, before any launch, what one launch
+    """rans_w64_gemv_group refuses, before any launch, what one launch
     cannot run: no matrices, more than 4, different cols or R, two states
     per lane, or split-K tilings."""
     x = ctypes.c_void_p(0x2000)
@@ -102,11 +102,11 @@ def test_group_validation_without_gpu(rans, lib):
     def call(descs, n=None, ys=None):
         arr = (ctypes.c_void_p * max(1, len(descs)))(*[ctypes.addressof(d) for d in descs])
         yarr = (ctypes.c_void_p * max(1, len(descs)))(*([0x3000] * len(descs) if ys is None else ys))
-        return lib.launch_rans_gemv_group(arr, len(descs) if n is None else n, x, 0, 1, yarr, None)
+        return lib.rans_w64_gemv_group(arr, len(descs) if n is None else n, x, 0, 1, yarr, None)
 
     a = _desc(rans, cols=2048)  # 8 column tiles: one workgroup per tile row
     b = _desc(rans, rows=512, cols=2048)
-    assert lib.launch_rans_gemv_group(None, 2, x, 0, 1, None, None) == -4
+    assert lib.rans_w64_gemv_group(None, 2, x, 0, 1, None, None) == -4
     assert call([a, b], n=0) == -4
     assert call([a] * 5) == -1
     assert call([a, _desc(rans, cols=4096, C=512)]) == -1  # different cols
@@ -152,7 +152,7 @@ def test_header_compiles_as_c(tmp_path):
     src = tmp_path / "use.c"
     src.write_text('#include "vramc_rans.h"\n'
                    "int main(void) { rans_w64_matrix m = {0}; (void)m;\n"
-                   "  return launch_rans_gemv_group ? 0 : 1; }\n")
+                   "  return rans_w64_gemv_group ? 0 : 1; }\n")
     for std, lang in (("c99", "c"), ("c++17", "c++")):
         subprocess.check_call([gcc, f"-std={std}", "-x", lang, "-fsyntax-only", f"-I{inc}",
                                "-I/opt/rocm/include", "-D__HIP_PLATFORM_AMD__", str(src)])

@@ -1,0 +1,122 @@
+"""The drop-in contract of encode(codes, R, C) on the CPU: every tiling the
+reference's own test and benchmark pass (kernel/bench.py:41-42 and the
+R/C sweep of kernel/bench.py:84-103) is accepted, mapped to a legal w64 tile
+and decoded back exactly, and the returned dict carries the reference's keys
+(kernel/rans.py:93-98) with the reference's meaning."""
+import ctypes
+
+import numpy as np
+import pytest
+
+# kernel/bench.py:41-42: (rows, cols, R, C, bits)
+REF_TEST = [(64, 256, 4, 256, 3.0), (128, 512, 8, 128, 2.0), (256, 1024, 16, 512, 4.0),
+            (32, 64, 1, 32, 1.0)]
+# kernel/bench.py:84-87
+REF_BENCH_SHAPES = {"1.5B qkv": (2048, 1536), "1.5B gate_up": (17920, 1536),
+                    "1.5B down": (1536, 8960), "27B-like attn": (5120, 5120),
+                    "27B-like gate_up": (34816, 5120), "27B-like down": (5120, 17408)}
+REF_KEYS = ("words", "offs", "table", "R", "C", "shape", "bits_payload", "bits_state_offs",
+            "bits_table", "entropy_model")
+
+
+def bench_sweep(rows, cols):
+    """(R, C) pairs of kernel/bench.py:100-103 for one shape."""
+    out = []
+    for R in (4, 8, 16):
+        for C in sorted({cols, 512, 1024, 2048} & set(range(32, cols + 1, 32))):
+            if cols % C or rows % R:
+                continue
+            out.append((R, C))
+    return out
+
+
+def _codes(rows, cols, seed, delta=0.45):
+    """round(Laplace(0,1)/delta) clipped to [-127, 127] (about 3 bits per
+    code), drawn by inverse CDF from 16-bit uniforms: fast at 178 M codes."""
+    rng = np.random.default_rng(seed)
+    u = (np.arange(65536) + 0.5) / 65536
+    lap = np.where(u < 0.5, np.log(2 * u), -np.log(2 - 2 * u))
+    lut = np.clip(np.round(lap / delta), -127, 127).astype(np.int32)
+    return lut[rng.integers(0, 65536, size=(rows, cols), dtype=np.uint16)]
+
+
+def _check_enc(rans, enc, codes, R, C):
+    rows, cols = codes.shape
+    for k in REF_KEYS:
+        assert k in enc, k
+    assert (enc["R"], enc["C"], tuple(enc["shape"])) == (R, C, (rows, cols))
+    tR, tC, tS = rans.tiling_of(enc)
+    # the mapped tile: a compiled height dividing R, a multiple of 64 within
+    # one (or, for C % 64 == 32, two) of the reference's tiles
+    assert R % tR == 0 and tR in rans.SUPPORTED_R
+    assert tC % (64 * tS) == 0 and cols % tC == 0 and (C if C % 64 == 0 else 2 * C) % tC == 0
+    assert tR * tC <= 65536 and tR * tC // (64 * tS) <= rans.MAX_STATE_SYMBOLS
+    # offs: one word offset per state (the reference's per-lane offs), each
+    # at its state's stream, which holds slen words, in state order
+    nstates = (rows // tR) * (cols // tC) * 64 * tS
+    assert enc["offs"].dtype == np.uint32 and enc["offs"].size == nstates
+    ends = enc["offs"].astype(np.int64) + enc["slen"]
+    ntiles = (rows // tR) * (cols // tC)
+    per_tile = ends.reshape(ntiles, -1)
+    starts = enc["offs"].astype(np.int64).reshape(ntiles, -1)
+    np.testing.assert_array_equal(starts[:, 1:], per_tile[:, :-1])
+    np.testing.assert_array_equal(starts[:, 0], enc["tile_off"][:-1])
+    assert np.all(per_tile[:, -1] < enc["tile_off"][1:])  # the pad word follows
+    assert np.array_equal(rans.decode_ref(enc), codes)
+
+
+@pytest.mark.parametrize("case", REF_TEST, ids=lambda c: "x".join(map(str, c[:4])))
+def test_reference_test_tilings(rans, oracle, case):
+    rows, cols, R, C, bits = case
+    codes = oracle.synth_codes(rows, cols, bits, seed=rows)
+    enc = rans.encode(codes, R, C)
+    _check_enc(rans, enc, codes, R, C)
+    # the reference's bit accounting keys keep their meaning: payload words
+    # over the weights, the 16 KB table over the weights
+    assert enc["bits_table"] == pytest.approx(32 * 4096 / codes.size)
+    assert enc["bits_payload"] >= 0
+
+
+@pytest.mark.parametrize("name", list(REF_BENCH_SHAPES))
+def test_reference_bench_sweep(rans, name):
+    """Every (R, C) of the sweep on the first 1024 rows of the shape (the
+    mapping depends on cols, R and C only; 1024 rows divide by every R of
+    the sweep), then the shape at full size with the sweep's first tiling."""
+    rows, cols = REF_BENCH_SHAPES[name]
+    codes = _codes(rows, cols, seed=rows + cols)
+    sweep = bench_sweep(rows, cols)
+    assert sweep
+    part = np.ascontiguousarray(codes[:1024])
+    for R, C in sweep:
+        _check_enc(rans, rans.encode(part, R, C), part, R, C)
+    R, C = sweep[0]
+    _check_enc(rans, rans.encode(codes, R, C), codes, R, C)
+
+
+def test_published_tilings_map(rans):
+    """The tilings of the published records (results/kernel_bench.json: e.g.
+    R=8, C=8960 at 1536x8960) and configuration 1's 32-lane R=512, C=256."""
+    cases = {(1536, 8960, 8, 8960): (8, 4480, 2), (5120, 5120, 16, 512): (16, 512, 1),
+             (34816, 5120, 4, 512): (4, 512, 1), (5120, 17408, 4, 512): (4, 512, 1),
+             (512, 256, 512, 256): (16, 256, 1), (32, 64, 1, 32): (1, 64, 1),
+             (17920, 1536, 8, 1536): (8, 1536, 1), (2048, 1536, 4, 512): (4, 512, 1),
+             (1536, 8960, 16, 8960): (16, 1792, 2)}
+    for (rows, cols, R, C), want in cases.items():
+        assert rans.w64_tiling(rows, cols, R, C) == want, (rows, cols, R, C)
+    # a legal w64 tiling maps to itself, whatever the state count
+    for rows, cols, R, C, S in ((1536, 8960, 3, 2240, 1), (8960, 1536, 35, 192, 1),
+                                (25600, 5120, 16, 640, 1), (1536, 8960, 8, 1792, 2),
+                                (1536, 8960, 16, 2240, 1)):
+        assert rans.w64_tiling(rows, cols, R, C, S) == (R, C, S)
+
+
+def test_reference_entry_points_refuse(rans):
+    """The reference's launch_rans_gemv / launch_rans_decode argument lists
+    (kernel/rans.py:25-29) reach entry points that return the reference's
+    "unsupported" code (-1) and touch nothing, instead of crashing."""
+    lib = ctypes.CDLL(rans.LIB)
+    for name in ("launch_rans_gemv", "launch_rans_decode"):
+        fn = getattr(lib, name)
+        fn.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
+        fn.restype = ctypes.c_int
+        assert fn(8, 1, 2, 3, 4, 5, 1536, 8960, 8960, None) == -1

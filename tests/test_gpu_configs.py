@@ -1,0 +1,159 @@
+"""Parity of the HIP path on the benchmark configurations' own workloads and
+on the reference's own tilings, through the C ABI, against the oracle.
+
+Bars as in test_gpu_parity: decoded codes bit-exact, bf16 decode bit-exact
+against bf16(code*step), GEMV relative L2 <= 1e-3 against the oracle's
+float64 dequant+GEMV (and the reference's max-abs-relative < 1e-4 where its
+test applies it, kernel/bench.py:55-56)."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-3
+
+
+@pytest.fixture(scope="module")
+def dev(rans):
+    if not torch.cuda.is_available():
+        raise RuntimeError("GPU tests need a ROCm device")
+    return torch.device("cuda")
+
+
+def _rel_l2(y, ref):
+    y = np.asarray(y, np.float64)
+    return float(np.linalg.norm(y - ref) / max(np.linalg.norm(ref), 1e-300))
+
+
+def _check(rans, oracle, lib, codes, R, C, step, x, x_bf16):
+    """encode(codes, R, C) with the reference's tiling, then every device
+    path against the oracle.  Returns the matrix."""
+    enc = rans.encode(codes, R, C)
+    m = rans.RansMatrix(enc, torch.from_numpy(step), lib)
+    np.testing.assert_array_equal(m.decode_codes().cpu().numpy(), codes)
+    want = (torch.from_numpy(codes.astype(np.float32)) * torch.from_numpy(step)).bfloat16()
+    assert torch.equal(m.decode().cpu().view(torch.int16), want.view(torch.int16))
+    xt = torch.from_numpy(x).cuda()
+    if x_bf16:
+        xt = xt.bfloat16()
+    y = m.gemv(xt).cpu().numpy().astype(np.float64)
+    ref = oracle.gemv_f64(codes, xt.float().cpu().numpy().astype(np.float64),
+                          step.astype(np.float64))
+    assert _rel_l2(y, ref) <= REL_L2, _rel_l2(y, ref)
+    return m, y, ref
+
+
+def test_config1_512x256(rans, oracle, lib, dev):
+    """Configuration 1 on the HIP path: 512x256 Laplace codes at 3.25 bits
+    (one per-tensor step), encoded with the reference's 32-lane tiling
+    R=512, C=256 (mapped to 16x256 tiles), f32 x ~ N(0,1), checked against
+    dense dequant.x as kernel/bench.py:38-56 does."""
+    import rans_bench as B
+    print("case config 1 512x256 R=512 C=256", flush=True)
+    codes = B.synth_codes_full(512, 256, 3.25, seed=512 + 256)
+    step = np.full(256, 0.0123, np.float32)
+    x = np.random.default_rng(1).standard_normal(256).astype(np.float32)
+    m, y, ref = _check(rans, oracle, lib, codes, 512, 256, step, x, x_bf16=False)
+    assert (m.R, m.C, m.S) == (16, 256, 1)
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-4
+
+
+@pytest.mark.parametrize("case", [(1536, 8960, 8, 8960, 3.25), (32, 64, 1, 32, 1.0),
+                                  (1536, 8960, 16, 8960, 3.25), (5120, 5120, 16, 512, 3.0)],
+                         ids=lambda c: "x".join(map(str, c[:4])))
+def test_reference_tilings(rans, oracle, lib, dev, case):
+    """The reference's own tilings through encode and the GPU: R=8, C=8960
+    (its published tiling of 1536x8960, results/kernel_bench.json:128-129),
+    its test shape 32x64 with R=1, C=32 (kernel/bench.py:42), and two more of
+    its sweep (kernel/bench.py:100-103), with log-normal steps and bf16 x."""
+    import rans_bench as B
+    rows, cols, R, C, bits = case
+    print(f"case reference tiling {case}", flush=True)
+    codes = B.synth_codes_full(rows, cols, bits, seed=rows + cols)
+    step = B.lognormal_steps(cols, seed=rows)
+    x = np.random.default_rng(2).standard_normal(cols).astype(np.float32)
+    _check(rans, oracle, lib, codes, R, C, step, x, x_bf16=True)
+
+
+CHAIN_LAYERS = int(os.environ.get("CHAIN_TEST_LAYERS", "4"))
+
+
+def test_config4_chain(rans, oracle, lib, dev):
+    """Configuration 4: the per-token chain of a Qwen2.5-1.5B-shaped weight
+    set at 3.25 bits (full-size layers, q/k/v and gate/up as grouped
+    launches), captured once in a HIP graph and replayed three times with
+    other device work in between.  Every matrix's output on every replay is
+    bitwise its own single launch and within the bar of the oracle."""
+    import rans_bench as B
+    L = CHAIN_LAYERS
+    print(f"case chain {L} layers grouped", flush=True)
+    ch = B.build_chain(bits=3.25, layers=L, seed=0, grouped=True, batch=1, tune=True,
+                       keep_codes=True, bf16=False, lib=lib)
+    mats = ch["mats"]
+    assert len(mats) == 7 * L and len(ch["launches"]) == 4 * L
+    assert any(len(launch) == 3 for launch in ch["launches"])  # q/k/v grouped
+    single = [m.gemv(ch["xs"][m.cols][0]).clone() for m in mats]
+    for i, m in enumerate(mats):
+        x = ch["xs"][m.cols][0].float().cpu().numpy().astype(np.float64)
+        ref = oracle.gemv_f64(ch["codes"][i], x, ch["steps"][i].astype(np.float64))
+        assert _rel_l2(single[i].cpu().numpy(), ref) <= REL_L2, (i, ch["names"][i])
+    ys = [torch.empty(1, m.rows, device="cuda") for m in mats]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        B.run_chain(ch, ys)  # first launches of each kernel outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        B.run_chain(ch, ys)
+    for rep in range(3):
+        for y in ys:
+            y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for i, y in enumerate(ys):
+            assert torch.equal(y[0], single[i]), (rep, i, ch["names"][i])
+        # eager work between replays
+        torch.randn(1 << 20, device="cuda").sum().item()
+
+
+def test_paired_rows_need_lds_for_both(rans, lib, dev):
+    """Two tile rows per workgroup hold both rows' staged blocks.  8192x10240
+    in 16x2560 tiles at 3.25 bits (512 tile rows, 4 waves of ~16.8 KB each)
+    fits one row per workgroup (~100 KB) but not two (~167 KB): the library
+    keeps one row per workgroup, the launch succeeds and matches the launch
+    forced onto the 4-byte table entries (never paired) bit for bit."""
+    import rans_bench as B
+    print("case paired rows LDS bound 8192x10240", flush=True)
+    rows, cols = 8192, 10240
+    codes = B.synth_codes_full(rows, cols, 3.25, seed=7)
+    step = torch.from_numpy(B.lognormal_steps(cols, seed=7))
+    enc = rans.encode(codes, 16, 2560, 1)
+    assert enc["max_tile_words"] > 8000
+    m = rans.RansMatrix(enc, step, lib, flags=rans.F_TABLE8)
+    m4 = rans.RansMatrix(enc, step, lib, flags=rans.F_TABLE4)
+    assert lib.rans_gemv_rows2(ctypes.byref(m._desc), rans.X_BF16, 1) == 0
+    x = torch.randn(cols, device="cuda").bfloat16()
+    assert torch.equal(m.gemv(x).cpu(), m4.gemv(x).cpu())
+
+
+def test_paired_rows_query(rans, lib, dev):
+    """rans_gemv_rows2 says which launches pair tile rows: 1536x8960 in
+    3x2240 tiles (512 tile rows, two per CU) does at batch 1 and 4; with the
+    4-byte table entries forced, or at S = 2, it does not."""
+    import rans_bench as B
+    print("case paired rows query", flush=True)
+    codes = B.synth_codes_full(1536, 8960, 3.25, seed=3)
+    step = torch.from_numpy(B.lognormal_steps(8960, seed=3))
+    m = rans.RansMatrix(rans.encode(codes, 3, 2240, 1), step, lib)
+    for batch in (1, 4):
+        assert lib.rans_gemv_rows2(ctypes.byref(m._desc), rans.X_BF16, batch) == 1
+    m4 = rans.RansMatrix(rans.encode(codes, 3, 2240, 1), step, lib, flags=rans.F_TABLE4)
+    assert lib.rans_gemv_rows2(ctypes.byref(m4._desc), rans.X_BF16, 1) == 0
+    m2 = rans.RansMatrix(rans.encode(codes, 3, 1792, 2), step, lib)
+    assert lib.rans_gemv_rows2(ctypes.byref(m2._desc), rans.X_BF16, 1) == 0

@@ -1,6 +1,6 @@
-"""Grouped GEMV launches (launch_rans_gemv_group through rans.gemv_group):
+"""Grouped GEMV launches (rans_w64_gemv_group through rans.gemv_group):
 several matrices that share x in one launch.  Each output must be bitwise
-the output of the matrix's own launch_rans_gemv, and within the GEMV bar of
+the output of the matrix's own rans_w64_gemv, and within the GEMV bar of
 the float64 oracle."""
 import ctypes
 
@@ -64,7 +64,7 @@ def test_group_of_four_and_launch_is_one(rans, oracle):
     descs = (ctypes.c_void_p * 4)(*[ctypes.addressof(m._desc) for m in mats])
     ys = [torch.empty(2, m.rows, device="cuda") for m in mats]
     yps = (ctypes.c_void_p * 4)(*[y.data_ptr() for y in ys])
-    rc = lib.launch_rans_gemv_group(descs, 4, x.data_ptr(), rans.X_BF16, 2, yps,
+    rc = lib.rans_w64_gemv_group(descs, 4, x.data_ptr(), rans.X_BF16, 2, yps,
                                     torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     for m, y in zip(mats, ys):
@@ -83,7 +83,7 @@ def test_group_falls_back_when_not_groupable(rans, oracle):
     descs = (ctypes.c_void_p * 2)(ctypes.addressof(a._desc), ctypes.addressof(b._desc))
     ys = [torch.empty(512, device="cuda") for _ in range(2)]
     yps = (ctypes.c_void_p * 2)(*[y.data_ptr() for y in ys])
-    assert a.lib.launch_rans_gemv_group(descs, 2, x.data_ptr(), rans.X_BF16, 1, yps,
+    assert a.lib.rans_w64_gemv_group(descs, 2, x.data_ptr(), rans.X_BF16, 1, yps,
                                         torch.cuda.current_stream().cuda_stream) == -1
     ya, yb = rans.gemv_group([a, b], x)
     assert torch.equal(ya, a.gemv(x)) and torch.equal(yb, b.gemv(x))

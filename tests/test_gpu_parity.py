@@ -259,25 +259,17 @@ def test_matrix_from_container_file(rans, oracle, lib, dev, tmp_path):
     np.testing.assert_array_equal(b.decode_codes().cpu().numpy(), codes)
 
 
-def _heavy_tail_codes(rows, cols, seed):
-    """Student-t(3) codes at about 3 bits with 1% escapes (|code| in
-    [128, 600)), generated fast enough for 131M weights."""
-    rng = np.random.default_rng(seed)
-    pool = np.rint(rng.standard_t(3, size=1 << 22) * 1.4).astype(np.int32)
-    codes = pool[rng.integers(0, pool.size, size=rows * cols)]
-    esc = rng.random(rows * cols) < 0.01
-    k = int(esc.sum())
-    codes[esc] = rng.integers(128, 600, size=k) * np.where(rng.random(k) < 0.5, -1, 1)
-    return codes.reshape(rows, cols)
-
-
 @pytest.mark.parametrize("rows,cols", [(25600, 5120), (5120, 25600)])
 def test_full_size_27b_shapes(rans, oracle, lib, dev, rows, cols):
-    """The 27B-class shapes at full size (131M weights, ~1.3M escapes):
-    every code bit-exact, GEMV at batch 1 and 4 against the float64 oracle,
-    both word-fetch policies bitwise equal."""
+    """The 27B-class shapes at full size (131M weights), the configuration's
+    own workload: Student-t(3) codes at 2.25 bits of full-tensor entropy
+    with 1% escapes (~1.3M, |code| in [128, 600)): every code bit-exact,
+    GEMV at batch 1 and 4 against the float64 oracle, both word-fetch
+    policies bitwise equal."""
+    import rans_bench as B
     print(f"case full size {rows}x{cols}", flush=True)
-    codes = _heavy_tail_codes(rows, cols, seed=rows)
+    codes = B.synth_codes_full(rows, cols, 2.25, dist="student3", seed=rows + cols,
+                               escape_frac=0.01)
     R, C = rans.pick_tiling(rows, cols)
     enc = rans.encode(codes, R, C, 1)
     step = np.exp(0.5 * np.random.default_rng(cols).standard_normal(cols)).astype(np.float32)
@@ -591,6 +583,10 @@ def test_two_tile_rows_odd_and_even(rans, oracle, lib, dev, tile_rows):
     enc = rans.encode(codes, 3, 2240, 1)
     m = rans.RansMatrix(enc, step, lib)
     m1 = rans.RansMatrix(enc, step, lib, flags=rans.F_TABLE4)
+    # the library's own answer: paired for the even count only
+    want = 1 if tile_rows % 2 == 0 else 0
+    assert lib.rans_gemv_rows2(ctypes.byref(m._desc), rans.X_BF16, 1) == want
+    assert lib.rans_gemv_rows2(ctypes.byref(m1._desc), rans.X_BF16, 1) == 0
     for batch in (1, 4):
         x = torch.randn(batch, cols, device="cuda").bfloat16()
         y = m.gemv(x).cpu()

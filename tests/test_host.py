@@ -150,26 +150,49 @@ def test_encode_rejects_bad_input(rans):
     with pytest.raises(AssertionError):
         rans.encode(ok, 3, 128)  # rows % R
     with pytest.raises(AssertionError):
-        rans.encode(ok, 4, 96)  # C % 64
+        rans.encode(ok, 4, 96)  # cols % C
     with pytest.raises(AssertionError):
-        rans.encode(ok, 4, 128, S=4)  # C % (64*S)
+        rans.encode(ok, 4, 80)  # C % 32 (the reference's own precondition)
+    with pytest.raises(AssertionError):
+        rans.encode(ok, 4, 128, S=4)  # no tile of the given S fits C % (64*S)
     with pytest.raises(AssertionError):
         rans.encode(np.zeros((0, 128), np.int32), 1, 128)
-    # a tile beyond 65536 codes (the side table's 16-bit positions)
-    big = np.random.default_rng(1).integers(-127, 128, size=(16, 65536)).astype(np.int32)
-    with pytest.raises(AssertionError, match="R\\*C"):
-        rans.encode(big, 16, 65536)
     # a code beyond the side table's 16-bit values
     for v in (32768, -32769, 2 ** 30):
         wide_code = ok.copy()
         wide_code[3, 5] = v
         with pytest.raises(AssertionError, match="32767"):
             rans.encode(wide_code, 4, 128)
-    # a state's stream beyond 255 words (1024 symbols of ~8 bits each), in
-    # a tile block that itself fits
+    # a state's stream beyond 255 words (1024 symbols of ~8 bits each) when
+    # the caller fixes one state per lane on a tile the format holds
     wide = np.random.default_rng(2).integers(-127, 128, size=(16, 4096)).astype(np.int32)
-    with pytest.raises(AssertionError):
-        rans.encode(wide, 16, 4096)
+    with pytest.raises(AssertionError, match="255"):
+        rans.encode(wide, 16, 4096, S=1)
+    # the encoder entry point itself refuses a tile beyond 65536 codes (the
+    # side table's 16-bit positions)
+    h = ctypes.c_void_p()
+    info = np.zeros(7, np.int64)
+    big = np.zeros((16, 8192), np.int32)
+    big[0, 0] = 1
+    rc = rans._host_lib().rans_w64_encode(rans._p(big), 16, 8192, 16, 8192, 1, 1,
+                                          ctypes.byref(h), rans._p(info))
+    assert rc == -2
+
+
+def test_encode_maps_oversized_requests(rans):
+    """Tilings beyond the format's limits are mapped, not refused: a tile of
+    more than 65536 codes becomes column sub-tiles, and states of more than
+    338 symbols get more states per lane; the round trip is exact."""
+    rng = np.random.default_rng(2)
+    wide = rng.integers(-127, 128, size=(16, 4096)).astype(np.int32)
+    enc = rans.encode(wide, 16, 4096)
+    assert (enc["R"], enc["C"]) == (16, 4096)
+    assert rans.tiling_of(enc) == (16, 4096, 4)
+    np.testing.assert_array_equal(rans.decode_ref(enc), wide)
+    big = rng.integers(-127, 128, size=(16, 65536)).astype(np.int32)
+    enc = rans.encode(big, 16, 65536)
+    assert rans.tiling_of(enc) == (16, 4096, 4)
+    np.testing.assert_array_equal(rans.decode_ref(enc), big)
 
 
 def test_stream_lengths_must_match(rans, oracle):

@@ -1181,10 +1181,15 @@ int device_cus() {
 // every CU a workgroup: 1536x1536 in 8x384 tiles (192 workgroups) ran 3-5%
 // slower as 96.  Single-matrix launches with one state per lane, one
 // workgroup per tile row (no split-K), at most 4 waves per row, an even
-// number of tile rows and the 8-byte table entries; not 35-row tiles.
-bool use_rows2(const rans_w64_matrix* m, int n, int v, int waves, int ngroups, int grid) {
+// number of tile rows and the 8-byte table entries; not 35-row tiles.  The
+// paired workgroup holds both rows' staged blocks, so it is only taken when
+// twice the dynamic LDS (lds bytes for one row's waves) still fits beside
+// the static arrays.
+bool use_rows2(const rans_w64_matrix* m, int n, int v, int waves, int ngroups, int grid,
+               size_t lds) {
     if (n != 1 || m->S != 1 || (v & 8) || m->R == 35 || ngroups != 1) return false;
     if (2 * waves > kMaxWaves || (m->rows / m->R) % 2) return false;
+    if (2 * lds + gemv_static_lds(m->R) > (size_t)kLdsMax) return false;
     const int cus = device_cus();
     return cus > 0 && grid >= 2 * cus;
 }
@@ -1347,7 +1352,7 @@ int launch_gemv_common(const rans_w64_matrix* const* ms, int n, const void* x, i
         if (n == 1)
             a.mat[0].table_lds =
                 reinterpret_cast<const uint4*>((v & 8) ? m0->table_lds4 : m0->table_lds);
-        const bool rows2 = use_rows2(m0, n, v, waves, ngroups, grid);
+        const bool rows2 = use_rows2(m0, n, v, waves, ngroups, grid, lds);
         if (rows2) v |= 16;
         a.W = rows2 ? 2 * waves : waves;
         const int rc = launch_gemv_fn(gemv_fn(m0->R, m0->S, B, v), a, a.W, rows2 ? 2 * lds : lds,
@@ -1373,7 +1378,7 @@ bool check_gemv_args(const rans_w64_matrix* m, const void* x, int x_dtype, int b
 
 }  // namespace
 
-extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
+extern "C" int rans_w64_gemv(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
                                 void* y, hipStream_t stream) {
     int rc = 0;
     if (!check_gemv_args(m, x, x_dtype, batch, y, rc)) return rc;
@@ -1381,7 +1386,7 @@ extern "C" int launch_rans_gemv(const rans_w64_matrix* m, const void* x, int x_d
     return launch_gemv_common(&m, 1, x, x_dtype, batch, ys, stream);
 }
 
-extern "C" int launch_rans_gemv_group(const rans_w64_matrix* const* ms, int n, const void* x,
+extern "C" int rans_w64_gemv_group(const rans_w64_matrix* const* ms, int n, const void* x,
                                       int x_dtype, int batch, float* const* ys,
                                       hipStream_t stream) {
     if (!ms || !ys || n <= 0) return RANS_EARG;
@@ -1425,11 +1430,45 @@ extern "C" int rans_gemv_table4(const rans_w64_matrix* m, int x_dtype, int batch
     return 0;
 }
 
-extern "C" int launch_rans_decode(const rans_w64_matrix* m, void* out_bf16, hipStream_t stream) {
+extern "C" int rans_gemv_rows2(const rans_w64_matrix* m, int x_dtype, int batch) {
+    if (!valid_geometry(m) || batch <= 0) return RANS_EGEOMETRY;
+    if (x_dtype != RANS_X_F32 && x_dtype != RANS_X_BF16) return RANS_EARG;
+    if (!supported_rs(m->R, m->S)) return RANS_EUNSUPPORTED;
+    const int waves = gemv_waves(m);
+    if (!waves) return RANS_EGEOMETRY;
+    const int fetch = m->flags & RANS_F_WORDS_MASK;
+    const bool refill = fetch == RANS_F_WORDS_REFILL || (fetch == 0 && m->R >= 3);
+    const int var = (x_dtype == RANS_X_BF16 ? 1 : 0) | (refill ? 2 : 0);
+    const size_t lds = (size_t)waves * wave_layout(m).raw_words * 2;
+    const int ngroups = (m->cols / m->C) / waves;
+    const int grid = (m->rows / m->R) * ngroups;
+    // the same per-chunk choices as launch_gemv_common: the table entries
+    // first (paired rows need the 8-byte ones), then the pairing
+    for (int B : {4, 1}) {
+        if ((B == 4 && batch < 2) || (B == 1 && batch % 4 != 1)) continue;
+        int v = var;
+        if ((m->flags & RANS_F_TABLE4 || m->table_lds4) && use_table4(m, B, var, waves, lds, grid))
+            v |= 8;
+        if (use_rows2(m, 1, v, waves, ngroups, grid, lds)) return 1;
+    }
+    return 0;
+}
+
+extern "C" int launch_rans_gemv(int, const void*, const void*, const void*, const void*, void*,
+                                int, int, int, hipStream_t) {
+    return RANS_EUNSUPPORTED;
+}
+
+extern "C" int launch_rans_decode(int, const void*, const void*, const void*, const void*, void*,
+                                  int, int, int, hipStream_t) {
+    return RANS_EUNSUPPORTED;
+}
+
+extern "C" int rans_w64_decode(const rans_w64_matrix* m, void* out_bf16, hipStream_t stream) {
     return launch_decode_common<1>(m, out_bf16, stream);
 }
 
-extern "C" int launch_rans_decode_codes(const rans_w64_matrix* m, int32_t* out, hipStream_t stream) {
+extern "C" int rans_w64_decode_codes(const rans_w64_matrix* m, int32_t* out, hipStream_t stream) {
     return launch_decode_common<0>(m, out, stream);
 }
 

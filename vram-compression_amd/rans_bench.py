@@ -303,25 +303,28 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
 CHAIN_GROUPS = {"q": "qkv", "k": "qkv", "v": "qkv", "gate": "mlp", "up": "mlp"}
 
 
-def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False, batch=1):
-    """Per-token chain of 7*layers batch-1 GEMVs over a random-init
-    Qwen2.5-1.5B-shaped weight set (one table per matrix, ECSQ-like Laplace
-    codes at `bits` bits/weight), graph-captured and replayed; the same chain
-    with bf16 F.linear.  Returns the total weight-pass latency of both.
+def build_chain(bits=3.25, layers=28, seed=0, grouped=False, batch=1, tune=True,
+                keep_codes=False, bf16=True, lib=None):
+    """The per-token chain's weight set: 7*layers matrices over a
+    random-init Qwen2.5-1.5B-shaped model (one table per matrix, ECSQ-like
+    Laplace codes at `bits` bits/weight, log-normal steps), encoded and
+    uploaded, and its launch sequence.
 
-    grouped: q, k, v and gate, up of a layer each run as one grouped launch
-    (gemv_group, tiled with pick_group_tiling); the bf16 chain then runs q, k,
-    v as one F.linear over the concatenated weights (faster than three),
-    gate and up separately (the concatenated shape is slower in rocBLAS).
-    batch: rows of x per GEMV (the same weights serve every row)."""
-    lib = rans.build()
+    grouped: q, k, v and gate, up of a layer are tiled for one grouped
+    launch each (pick_group_tiling).  tune: the word-fetch policy is timed
+    once per shape, on the first layer.  keep_codes: keep each matrix's
+    codes and step on the host (for a parity check).  bf16: also build the
+    bf16 weights of the comparator chain.
+
+    Returns a dict: mats (RansMatrix, chain order), names, launches (lists
+    of matrix indices, one per launch), xs (one bf16 activation per cols, of
+    `batch` rows), codes/steps (with keep_codes), Ws (bf16 weights), nbytes,
+    nweights."""
+    lib = lib or rans.build()
     rng = np.random.default_rng(seed)
-    mats, Ws, xs = [], [], {}
-    nbytes = 0
-    nweights = 0
-    # one step per shape, chosen on a sample, so every layer has ~`bits` bits
-    deltas = {}
-    fetch = {}
+    mats, names, launches, codes_l, steps_l, Ws, xs = [], [], [], [], [], [], {}
+    nbytes = nweights = 0
+    deltas, fetch = {}, {}
     shapes = qwen15b_layer_shapes()
     tiling = {name: chain_tiling(rows, cols) for name, rows, cols in shapes}
     if grouped:
@@ -330,7 +333,7 @@ def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False, batch=1):
             t = pick_group_tiling([r for _, r, _ in members], members[0][2])
             for n, _, _ in members:
                 tiling[n] = t
-    steps = []  # launches in chain order: lists of (name, matrix)
+    # one step per shape, chosen on a sample, so every layer has ~`bits` bits
     for name, rows, cols in shapes:
         sample = rng.laplace(size=1 << 20)
         lo, hi = -12.0, 6.0
@@ -342,57 +345,92 @@ def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False, batch=1):
     for layer in range(layers):
         for name, rows, cols in shapes:
             codes = np.round(rng.laplace(size=(rows, cols)) / deltas[name]).astype(np.int32)
-            step = torch.from_numpy(lognormal_steps(cols, seed=seed + layer))
+            stepv = lognormal_steps(cols, seed=seed + layer)
             R, C = tiling[name]
             enc = encode(codes, R, C, 1)
             # word-fetch policy tuned once per shape, on the first layer
-            m = rans.RansMatrix(enc, step, lib, flags=fetch.get(name, 0))
+            m = rans.RansMatrix(enc, torch.from_numpy(stepv), lib, flags=fetch.get(name, 0))
             if name not in fetch:
-                fetch[name] = m.tune()
+                fetch[name] = m.tune() if tune else m.flags & rans.F_WORDS_MASK
+            i = len(mats)
             mats.append(m)
+            names.append(name)
             g = CHAIN_GROUPS.get(name) if grouped else None
-            if g and steps and CHAIN_GROUPS.get(steps[-1][0][0]) == g \
-                    and len(steps[-1]) < rans.GROUP_MAX:
-                steps[-1].append((name, m))
+            if g and launches and CHAIN_GROUPS.get(names[launches[-1][0]]) == g \
+                    and len(launches[-1]) < rans.GROUP_MAX:
+                launches[-1].append(i)
             else:
-                steps.append([(name, m)])
+                launches.append([i])
             nbytes += m.nbytes
             nweights += codes.size
-            Ws.append((torch.from_numpy(codes.astype(np.float32)) * step).bfloat16().cuda())
+            if keep_codes:
+                codes_l.append(codes)
+                steps_l.append(stepv)
+            if bf16:
+                Ws.append((torch.from_numpy(codes.astype(np.float32)) *
+                           torch.from_numpy(stepv)).bfloat16().cuda())
             if cols not in xs:
                 xs[cols] = torch.randn(batch, cols, device="cuda").bfloat16()
             print(f"chain: layer {layer} {name} encoded", file=sys.stderr, flush=True) \
                 if name == "down" and layer % 7 == 0 else None
-    ys = {n: torch.empty(batch, r, device="cuda") for n, r, _ in shapes}
+    return dict(mats=mats, names=names, launches=launches, xs=xs, codes=codes_l,
+                steps=steps_l, Ws=Ws, nbytes=nbytes, nweights=nweights, batch=batch)
+
+
+def run_chain(ch, ys):
+    """Issues the chain's launches on the current stream: ys[i] receives
+    matrix i's product (several matrices may share one buffer)."""
+    mats = ch["mats"]
+    for launch in ch["launches"]:
+        if len(launch) > 1:
+            gemv_group([mats[i] for i in launch], ch["xs"][mats[launch[0]].cols],
+                       [ys[i] for i in launch])
+        else:
+            m = mats[launch[0]]
+            m.gemv(ch["xs"][m.cols], ys[launch[0]])
+
+
+def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False, batch=1):
+    """Per-token chain of 7*layers batch-1 GEMVs over a random-init
+    Qwen2.5-1.5B-shaped weight set (build_chain), graph-captured and
+    replayed; the same chain with bf16 F.linear.  Returns the total
+    weight-pass latency of both.
+
+    grouped: q, k, v and gate, up of a layer each run as one grouped launch
+    (gemv_group, tiled with pick_group_tiling); the bf16 chain then runs q, k,
+    v as one F.linear over the concatenated weights (faster than three),
+    gate and up separately (the concatenated shape is slower in rocBLAS).
+    batch: rows of x per GEMV (the same weights serve every row)."""
+    ch = build_chain(bits, layers, seed, grouped, batch)
+    mats, names = ch["mats"], ch["names"]
+    # one output buffer per projection name, reused by every layer
+    ybuf = {}
+    for m, n in zip(mats, names):
+        ybuf.setdefault(n, torch.empty(batch, m.rows, device="cuda"))
+    ys = [ybuf[n] for n in names]
+    Ws = ch["Ws"]
     if grouped:  # q, k, v weights of a layer concatenated for the bf16 chain
-        Wl, i = [], 0
-        for step_ in steps:
-            ws = Ws[i:i + len(step_)]
-            i += len(step_)
-            if CHAIN_GROUPS.get(step_[0][0]) == "qkv":
+        Wl = []
+        for launch in ch["launches"]:
+            ws = [Ws[i] for i in launch]
+            if CHAIN_GROUPS.get(names[launch[0]]) == "qkv":
                 Wl.append(torch.cat(ws, 0).contiguous())
             else:
                 Wl.extend(ws)
         Ws = Wl
-
-    def run_rans():
-        for step_ in steps:
-            if len(step_) > 1:
-                gemv_group([m for _, m in step_], xs[step_[0][1].cols], [ys[n] for n, _ in step_])
-            else:
-                n, m = step_[0]
-                m.gemv(xs[m.cols], ys[n])
+    xs = ch["xs"]
 
     def run_bf16():
         for W in Ws:
             torch.nn.functional.linear(xs[W.shape[1]], W)
 
-    t_rans = timeit_graph(run_rans, iters, warmup=2)
+    t_rans = timeit_graph(lambda: run_chain(ch, ys), iters, warmup=2)
     t_bf16 = timeit_graph(run_bf16, iters, warmup=2)
+    nweights, nbytes = ch["nweights"], ch["nbytes"]
     return dict(config=f"Qwen2.5-1.5B-shaped weight set, {layers} layers x 7 matrices, "
                 f"batch {batch}" + (", q/k/v and gate/up grouped" if grouped else ""),
-                gemvs=len(mats), launches=len(steps), weights=nweights, bits_target=bits,
-                bits_total=8 * nbytes / nweights, compressed_MB=nbytes / 1e6,
+                gemvs=len(mats), launches=len(ch["launches"]), weights=nweights,
+                bits_target=bits, bits_total=8 * nbytes / nweights, compressed_MB=nbytes / 1e6,
                 bf16_MB=nweights * 2 / 1e6, t_rans_us=t_rans, t_bf16_us=t_bf16,
                 effective_GBps=nweights * 2 / t_rans / 1e3, speedup_vs_bf16=t_bf16 / t_rans)
 

@@ -19,6 +19,7 @@ Layout (all integers little endian, every section 64-byte aligned):
     index, nmat records of 256 bytes
         name       64 bytes UTF-8, NUL padded
         rows, cols, R, C, S, max_tile_words, max_state_words, flags   i32 x 8
+                   (R, C, S: the w64 tiling, tile_R/tile_C/S of the enc dict)
         nwords, ntiles, nstates, nesc, payload_words                  u64 x 5
         entropy_model                                                 f64
         offsets of words, tile_off, slen, states, table, esc_tileptr,
@@ -93,7 +94,7 @@ def save(path, entries):
             pos = _align(pos + len(b))
         name = e["name"].encode("utf-8")
         assert len(name) <= 64, "matrix names are at most 64 bytes of UTF-8"
-        recs.append(_RECORD.pack(name, rows, cols, enc["R"], enc["C"], enc["S"],
+        recs.append(_RECORD.pack(name, rows, cols, *rans.tiling_of(enc),
                                  enc["max_tile_words"], enc["max_state_words"],
                                  int(e.get("flags", 0)), arrays["words"].size,
                                  arrays["tile_off"].size - 1, arrays["states"].size,
@@ -116,7 +117,8 @@ def save(path, entries):
 def load(path, verify=True, mmap=True):
     """Read a container written by `save`.  Returns a list of dicts with
     keys name, enc (the dict rans.encode returns, arrays as read-only views
-    of the file when mmap), step and flags.  Raises ValueError on a wrong
+    of the file when mmap; its R and C are the stored w64 tiling, since the
+    tiling the encoder was asked for is not kept), step and flags.  Raises ValueError on a wrong
     magic or version, a truncated file, a section outside the file, or (with
     verify) a CRC mismatch."""
     size = os.path.getsize(path)
@@ -167,12 +169,14 @@ def load(path, verify=True, mmap=True):
         enc = dict(words=arrays["words"], tile_off=arrays["tile_off"], slen=arrays["slen"],
                    states=arrays["states"], table=arrays["table"],
                    esc_tileptr=arrays["esc_tileptr"], esc_pos=arrays["esc_pos"],
-                   esc_val=arrays["esc_val"], R=R, C=C, S=S, shape=(rows, cols),
+                   esc_val=arrays["esc_val"], R=R, C=C, tile_R=R, tile_C=C, S=S,
+                   shape=(rows, cols),
                    max_tile_words=mtw, max_state_words=msw,
                    bits_payload=16 * payload_words / N,
                    bits_state_offs=(40 * nstates + 32 * (ntiles + 1) + 16 * pad) / N,
                    bits_table=32 * rans.M / N,
                    bits_escape=(32 * (ntiles + 1) + 32 * nesc) / N,
                    entropy_model=entropy_model)
+        enc["offs"] = rans.stream_offsets(enc)
         out.append(dict(name=name, enc=enc, step=arrays["step"], flags=flags))
     return out
