@@ -73,6 +73,15 @@ extern "C" {
 #define RANS_ECODES (-5)       /* encoder: degenerate or empty symbol distribution, or a
                                   code outside [-32768, 32767] */
 #define RANS_ETILE (-6)        /* encoder: a tile block exceeds 65535 words, or a state 255 */
+#define RANS_ESCRATCH (-7)     /* rans_w64_gemv_noalloc: the launch needs more split-K
+                                  scratch than the library holds (RANS_SCRATCH_BYTES) */
+
+/* The scratch array of rans_w64_gemv_noalloc, one per GPU: arrival counters
+ * (one u32 per tile row, so at most 16384 tile rows), then split-K partial
+ * sums (4 bytes per output row, column group and batch row of a batch-4
+ * chunk, so at most 4128768 bytes of them). */
+#define RANS_SCRATCH_BYTES (4 << 20)
+#define RANS_SCRATCH_COUNTER_BYTES (64 << 10)
 
 /* rans_w64_matrix.flags.  Word fetch (bits 0-1): how the GEMV fetches
  * renormalisation words; the decoded values are identical, only speed
@@ -144,6 +153,22 @@ int64_t rans_gemv_workspace_bytes(const rans_w64_matrix* m, int batch);
  * Uses the current device's CU count; launches nothing.  No reference
  * counterpart. */
 int rans_gemv_rows2(const rans_w64_matrix* m, int x_dtype, int batch);
+
+/* rans_w64_gemv without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No reference counterpart.  The same
+ * kernels and the same results, bit for bit; m->workspace is ignored: the
+ * split-K partial sums and arrival counters live in a file-scope device
+ * array of RANS_SCRATCH_BYTES per GPU, held until the process ends.  Calls
+ * no allocating routine.  The first call on a device looks the array up and
+ * clears its counters with a fill kernel on `stream`; every launch leaves
+ * them at zero.  Every call on one GPU shares that GPU's array, so calls
+ * that overlap on one GPU (two streams, or two host threads) race: the
+ * caller serialises them.  Returns RANS_ESCRATCH, before touching the
+ * device, when the launch needs more than 16384 tile rows of counters or
+ * more partials than the array holds. */
+int rans_w64_gemv_noalloc(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
+                          void* y, hipStream_t stream);
 
 /* rans_w64_gemv for n <= 4 matrices that share x, in one launch:
  * ys[i] (batch x ms[i]->rows f32) gets ms[i]'s product.  No reference

@@ -1284,18 +1284,33 @@ extern "C" int64_t rans_gemv_workspace_bytes(const rans_w64_matrix* m, int batch
 
 namespace {
 
+// Split-K buffers of one launch: the arrival counters (one per tile row,
+// zero between launches) and the partial sums.
+struct SplitK {
+    uint32_t* counters;
+    float* partial;
+};
+
+// The split-K buffers in the matrix's own workspace (counters first, then
+// the partials), or {nullptr, nullptr} when it is missing or too small.
+SplitK workspace_splitk(const rans_w64_matrix* m, int batch) {
+    if (!m->workspace || m->workspace_bytes < rans_gemv_workspace_bytes(m, batch))
+        return {nullptr, nullptr};
+    return {static_cast<uint32_t*>(m->workspace),
+            reinterpret_cast<float*>(static_cast<uint8_t*>(m->workspace) + counters_bytes(m))};
+}
+
 // One launch over n matrices that share x (n = 1: any single matrix,
-// split-K included; n > 1: a group, validated by the caller).
+// split-K included, with its buffers in sk; n > 1: a group, validated by
+// the caller, never split).
 int launch_gemv_common(const rans_w64_matrix* const* ms, int n, const void* x, int x_dtype,
-                       int batch, float* const* ys, hipStream_t stream) {
+                       int batch, float* const* ys, hipStream_t stream, SplitK sk) {
     const rans_w64_matrix* m0 = ms[0];
     const int waves = gemv_waves(m0);
     if (!waves) return RANS_EGEOMETRY;
     const int ncb0 = m0->cols / m0->C;
     const int ngroups = ncb0 / waves;
-    if (ngroups > 1 &&
-        (!m0->workspace || m0->workspace_bytes < rans_gemv_workspace_bytes(m0, batch)))
-        return RANS_EWORKSPACE;
+    if (ngroups > 1 && (!sk.counters || !sk.partial)) return RANS_EWORKSPACE;
     const bool xbf16 = x_dtype == RANS_X_BF16;
     const size_t xsz = xbf16 ? 2 : 4;
     const int fetch = m0->flags & RANS_F_WORDS_MASK;
@@ -1307,10 +1322,8 @@ int launch_gemv_common(const rans_w64_matrix* const* ms, int n, const void* x, i
     a.cols = m0->cols;
     a.ngroups = ngroups;
     a.W = waves;
-    a.counters = ngroups > 1 ? static_cast<uint32_t*>(m0->workspace) : nullptr;
-    a.partial = ngroups > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(m0->workspace) +
-                                                       counters_bytes(m0))
-                            : nullptr;
+    a.counters = ngroups > 1 ? sk.counters : nullptr;
+    a.partial = ngroups > 1 ? sk.partial : nullptr;
     int grid = 0;
     a.wave_words = 0;
     for (int i = 0; i < n; i++) {
@@ -1383,7 +1396,7 @@ extern "C" int rans_w64_gemv(const rans_w64_matrix* m, const void* x, int x_dtyp
     int rc = 0;
     if (!check_gemv_args(m, x, x_dtype, batch, y, rc)) return rc;
     float* ys[1] = {static_cast<float*>(y)};
-    return launch_gemv_common(&m, 1, x, x_dtype, batch, ys, stream);
+    return launch_gemv_common(&m, 1, x, x_dtype, batch, ys, stream, workspace_splitk(m, batch));
 }
 
 extern "C" int rans_w64_gemv_group(const rans_w64_matrix* const* ms, int n, const void* x,
@@ -1408,7 +1421,7 @@ extern "C" int rans_w64_gemv_group(const rans_w64_matrix* const* ms, int n, cons
         if (lds_bytes(waves, wave_layout(m)) + gemv_static_lds(m->R) > (size_t)kLdsMax)
             return RANS_EGEOMETRY;
     }
-    return launch_gemv_common(ms, n, x, x_dtype, batch, ys, stream);
+    return launch_gemv_common(ms, n, x, x_dtype, batch, ys, stream, SplitK{nullptr, nullptr});
 }
 
 extern "C" int rans_gemv_table4(const rans_w64_matrix* m, int x_dtype, int batch) {
@@ -1480,4 +1493,78 @@ extern "C" int launch_int4_gemv(const void* w, const void* x, void* y, int rows,
                        static_cast<const uint32_t*>(w), static_cast<const float*>(x),
                        static_cast<float*>(y), rows, cols);
     return (int)hipGetLastError();
+}
+
+// ------------------------------------------------ allocation-free GEMV entry
+// rans_w64_gemv_noalloc runs split-K launches with the partial sums and the
+// arrival counters in this file-scope array instead of the matrix's
+// workspace: one array per GPU, held until the process ends, shared by every
+// call on that GPU (so calls that overlap on one GPU race).  Layout: the
+// counters (RANS_SCRATCH_COUNTER_BYTES, one u32 per tile row, zero between
+// launches), then the partials.  Host code never passes the array's name to
+// a kernel: on the host it is a stand-in, not a device address.  Its device
+// address comes from hipGetSymbolAddress, once per device.
+namespace {
+
+static __device__ __align__(256) uint8_t scratch[RANS_SCRATCH_BYTES];
+
+__global__ void __launch_bounds__(256) zero_u32_kernel(uint32_t* p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kScratchDevices];
+
+// The scratch array's device address on the current device.  The first call
+// on a device looks it up and clears the counters with a fill kernel on
+// `stream` (a kernel, so that a call under graph capture records a kernel
+// node); every GEMV leaves the counters it used at zero again.
+int scratch_base(hipStream_t stream, uint8_t** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kScratchDevices) return RANS_EUNSUPPORTED;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!p) return RANS_EARG;
+        constexpr int n = RANS_SCRATCH_COUNTER_BYTES / 4;
+        hipLaunchKernelGGL(zero_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, stream,
+                           static_cast<uint32_t*>(p), n);
+        e = hipGetLastError();
+        if (e != hipSuccess) return (int)e;
+        g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int rans_w64_gemv_noalloc(const rans_w64_matrix* m, const void* x, int x_dtype,
+                                     int batch, void* y, hipStream_t stream) {
+    int rc = 0;
+    if (!check_gemv_args(m, x, x_dtype, batch, y, rc)) return rc;
+    const int64_t need = rans_gemv_workspace_bytes(m, batch);
+    if (need < 0) return (int)need;
+    SplitK sk{nullptr, nullptr};
+    if (need > 0) {
+        // the sizes are checked before anything touches the device
+        const int64_t counters = (int64_t)(m->rows / m->R) * 4;
+        const int64_t partials = need - (int64_t)counters_bytes(m);
+        if (counters > RANS_SCRATCH_COUNTER_BYTES ||
+            partials > (int64_t)RANS_SCRATCH_BYTES - RANS_SCRATCH_COUNTER_BYTES)
+            return RANS_ESCRATCH;
+        uint8_t* base = nullptr;
+        rc = scratch_base(stream, &base);
+        if (rc != 0) return rc;
+        sk = {reinterpret_cast<uint32_t*>(base),
+              reinterpret_cast<float*>(base + RANS_SCRATCH_COUNTER_BYTES)};
+    }
+    float* ys[1] = {static_cast<float*>(y)};
+    return launch_gemv_common(&m, 1, x, x_dtype, batch, ys, stream, sk);
 }
