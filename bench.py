@@ -66,14 +66,9 @@ def algorithmic_bytes(enc, rows, cols, batch=1):
 
 
 def copies_for(steps, nbytes):
-    """Distinct copies of an nbytes operand for a rotated run of `steps`
-    launches: n512 = ceil(512 MiB / nbytes) copies when steps >= n512 (the
-    timed launches cycle through them, so every copy is read again only
-    after >= 512 MiB of other copies), else steps + n512 (the timed launches
-    use the first `steps`, an untimed flush replay reads the other n512
-    just before them)."""
-    n512 = max(2, -(-ROTATE_BYTES // nbytes))
-    return n512 if steps >= n512 else steps + n512
+    """Copies of an nbytes operand for `steps` rotated launches
+    (rans_bench.copies_for with the 512 MiB rotation)."""
+    return B.copies_for(steps, nbytes, ROTATE_BYTES)
 
 
 def graph_time_us(fns, steps, warmup, rotate=None):
@@ -234,6 +229,8 @@ def main():
     ap.add_argument("--no-rocblas", action="store_true")
     ap.add_argument("--no-chain", action="store_true",
                     help="skip the per-token chain (196 GEMVs, grouped launches)")
+    ap.add_argument("--no-ecsq", action="store_true",
+                    help="skip the row with ECSQ-GPTQ + waterfilling code statistics")
     ap.add_argument("--sweep", action="store_true", help="print a tiling sweep to stderr")
     ap.add_argument("--profile", action="store_true",
                     help="for rocprofv3: K eager launches of the headline GEMV over the rotating "
@@ -367,6 +364,22 @@ def main():
                  "workload": r["config"]}
         torch.cuda.empty_cache()
 
+    # codes with ECSQ-GPTQ + waterfilling statistics (the k projection of a
+    # synthetic layer quantised by the reference's method, tiled to the q/k/v
+    # group's 2048x1536) with their own per-column steps, batch 1
+    ecsq = None
+    if not args.no_ecsq:
+        codes_e, step_e = B.ecsq_fixture(rows=2048)
+        r = B.config_matrix(2048, 1536, 3.25, "ecsq_wf", 0.0, 1, 0, lib, codes=codes_e,
+                            step=step_e, iters=args.steps)
+        ecsq = {k: r[k] for k in ("rows", "cols", "R", "C", "entropy", "bits_total", "n_escapes",
+                                  "t_rans_us", "t_bf16_us", "effective_GBps", "speedup_vs_bf16",
+                                  "rel_l2_vs_f64", "copies")}
+        ecsq["workload"] = ("q/k/v-shaped 2048x1536 ECSQ-GPTQ + waterfilling codes at 3.25 b/w "
+                            "(246 levels, escapes up to |196|), own per-column steps, bf16 x, "
+                            "batch 1")
+        torch.cuda.empty_cache()
+
     achieved = alg / (t_rot * 1e-6) / 1e9
     fetch_name = {rans.F_WORDS_ALWAYS: "always", rans.F_WORDS_REFILL: "refill"}.get(measure.flags & 3)
     pmc = PMC_TRAFFIC_KIB.get((R, C, S, fetch_name))
@@ -406,6 +419,7 @@ def main():
                      "kernel": "rans_w64_gemv_kernel", "bytes_per_launch": alg},
         "cpu_baseline": cpu,
         "chain": chain,
+        "ecsq_wf": ecsq,
     }
     print(json.dumps(out), flush=True)
 

@@ -79,7 +79,7 @@ def test_reference_tilings(rans, oracle, lib, dev, case):
     _check(rans, oracle, lib, codes, R, C, step, x, x_bf16=True)
 
 
-CHAIN_LAYERS = int(os.environ.get("CHAIN_TEST_LAYERS", "4"))
+CHAIN_LAYERS = int(os.environ.get("CHAIN_TEST_LAYERS", "28"))
 
 
 def test_config4_chain(rans, oracle, lib, dev):
@@ -157,3 +157,23 @@ def test_paired_rows_query(rans, lib, dev):
     assert lib.rans_gemv_rows2(ctypes.byref(m4._desc), rans.X_BF16, 1) == 0
     m2 = rans.RansMatrix(rans.encode(codes, 3, 1792, 2), step, lib)
     assert lib.rans_gemv_rows2(ctypes.byref(m2._desc), rans.X_BF16, 1) == 0
+
+
+def test_ecsq_wf_fixture(rans, oracle, lib, dev):
+    """Codes with ECSQ-GPTQ + waterfilling statistics (tests/golden/
+    ecsq_wf_kv.npz: 246 levels, 24 escapes up to |196|) with their own
+    per-column steps: every device path against the oracle, alone and tiled
+    eight times into the q/k/v group's 2048x1536 shape (the configuration
+    row of rans_bench.configs)."""
+    import rans_bench as B
+    print("case ecsq-wf fixture", flush=True)
+    codes, step = B.ecsq_fixture()
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal(codes.shape[1]).astype(np.float32)
+    _check(rans, oracle, lib, codes, *rans.pick_tiling(*codes.shape), step, x, x_bf16=True)
+    big, step = B.ecsq_fixture(rows=2048)
+    m, _, _ = _check(rans, oracle, lib, big, *rans.pick_tiling(*big.shape), step, x, x_bf16=True)
+    xb = torch.randn(4, big.shape[1], device="cuda").bfloat16()
+    ref = oracle.gemv_f64(big, xb.float().cpu().numpy().astype(np.float64),
+                          step.astype(np.float64))
+    assert _rel_l2(m.gemv(xb).cpu().numpy(), ref) <= REL_L2

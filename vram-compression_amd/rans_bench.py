@@ -109,6 +109,25 @@ def synth_codes_full(rows, cols, target_bits, dist="laplace", seed=0, escape_fra
     return codes
 
 
+ECSQ_FIXTURE = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                            "tests", "golden", "ecsq_wf_kv.npz")
+
+
+def ecsq_fixture(rows=None):
+    """Codes with ECSQ-GPTQ + waterfilling statistics and their per-column
+    steps: the k projection (256 x 1536) of a synthetic random-init
+    Qwen2.5-1.5B layer quantised at 3.25 b/w by a restatement of the
+    reference's ecsq_wf method (exp/quant.py:116-156; written by
+    tests/golden/make_ecsq_golden.py).  rows: a multiple of 256, the 256 rows
+    repeated to that height.  Returns (int32 codes, float32 steps)."""
+    z = np.load(ECSQ_FIXTURE)
+    codes = z["codes"].astype(np.int32)
+    if rows is not None:
+        assert rows % codes.shape[0] == 0, "rows must be a multiple of 256"
+        codes = np.tile(codes, (rows // codes.shape[0], 1))
+    return np.ascontiguousarray(codes), z["step"].astype(np.float32)
+
+
 def lognormal_steps(cols, sigma=0.5, seed=0, scale=0.01):
     """Per-column waterfilling steps scale*exp(sigma*N(0,1))."""
     rng = np.random.default_rng(seed + 1)
@@ -131,10 +150,25 @@ def timeit(fn, iters=200):
     return s.elapsed_time(e) / iters * 1000
 
 
-def timeit_graph(fns, iters=200, warmup=10):
+def copies_for(iters, nbytes, rotate_bytes=512 << 20):
+    """Distinct copies of an nbytes operand for a rotated run of `iters`
+    launches: n = ceil(rotate_bytes / nbytes) copies when iters >= n (the
+    timed launches cycle through them, so every copy is read again only after
+    rotate_bytes of other copies), else iters + n (the timed launches use
+    the first iters copies; an untimed flush replay reads the other n just
+    before them)."""
+    n = max(2, -(-rotate_bytes // nbytes))
+    return n if iters >= n else iters + n
+
+
+def timeit_graph(fns, iters=200, warmup=10, rotate=False):
     """Device time per call: fns (one callable, or a list cycled through, e.g.
     one per rotating copy) are captured `iters` times in a HIP graph; the
     graph is replayed once untimed and then timed between HIP events.
+    rotate (fns sized by copies_for): when iters is below len(fns), the timed
+    graph runs calls 0..iters-1 and an untimed graph of all the other calls
+    runs just before the timed replay, so every timed call reads a copy that
+    the other copies have displaced from the caches.
     Returns microseconds per call."""
     if callable(fns):
         fns = [fns]
@@ -152,7 +186,15 @@ def timeit_graph(fns, iters=200, warmup=10):
     with torch.cuda.graph(g):
         for i in range(iters):
             fns[i % len(fns)]()
+    flush = None
+    if rotate and iters < len(fns):
+        flush = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(flush):
+            for f in fns[iters:]:
+                f()
     g.replay()
+    if flush is not None:
+        flush.replay()
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
@@ -162,7 +204,6 @@ def timeit_graph(fns, iters=200, warmup=10):
     return s.elapsed_time(e) / iters * 1000
 
 
-# ---------------------------------------------------------------- harness
 def test():
     """The reference's test (bench.py:38-66) on the w64 layout."""
     lib = rans.build()
@@ -264,27 +305,34 @@ def chain_tiling(rows, cols):
 
 
 def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None, C=None, S=1,
-                  iters=100, rotate_bytes=512 << 20):
+                  iters=100, rotate_bytes=512 << 20, codes=None, step=None):
     """Times one encoded matrix (rotated over >= rotate_bytes of copies) and
-    the bf16 F.linear on the same shape and rotation; checks the GEMV."""
-    codes = synth_codes_full(rows, cols, bits, dist=dist, seed=seed, escape_frac=escape_frac)
-    step = torch.from_numpy(lognormal_steps(cols, seed=seed))
+    the bf16 F.linear on the same shape and rotation; checks the GEMV.
+    codes/step: a given matrix and its steps instead of synthetic ones."""
+    if codes is None:
+        codes = synth_codes_full(rows, cols, bits, dist=dist, seed=seed, escape_frac=escape_frac)
+        step = torch.from_numpy(lognormal_steps(cols, seed=seed))
+    else:
+        step = torch.from_numpy(np.asarray(step, np.float32))
     if R is None or C is None:
         R, C = pick_tiling(rows, cols, S=S)
     enc = encode(codes, R, C, S)
     m = rans.RansMatrix(enc, step, lib)
     flags = m.tune(batch=batch)
-    ncopy = max(2, -(-rotate_bytes // m.nbytes))
+    ncopy = copies_for(iters, m.nbytes, rotate_bytes)
     ms = [m] + [rans.RansMatrix(enc, step, lib, flags=flags) for _ in range(ncopy - 1)]
     x = torch.randn(batch, cols, device="cuda").bfloat16()
     y = torch.empty(batch, rows, device="cuda")
-    t_rans = timeit_graph([lambda mm=mm: mm.gemv(x, y) for mm in ms], iters)
-    nW = max(2, -(-rotate_bytes // (rows * cols * 2)))
+    t_rans = timeit_graph([lambda mm=mm: mm.gemv(x, y) for mm in ms], iters, rotate=True)
+    nW = copies_for(iters, rows * cols * 2, rotate_bytes)
     W = (torch.from_numpy(codes.astype(np.float32)) * step).bfloat16().cuda()
     Ws = [W] + [W.clone() for _ in range(nW - 1)]
-    t_bf16 = timeit_graph([lambda Wd=Wd: torch.nn.functional.linear(x, Wd) for Wd in Ws], iters)
-    ref = torch.nn.functional.linear(x.float(), W.float())
-    got = ms[0].gemv(x)
+    t_bf16 = timeit_graph([lambda Wd=Wd: torch.nn.functional.linear(x, Wd) for Wd in Ws], iters,
+                          rotate=True)
+    # against the exact product codes @ (x * step) in float64 (the bf16
+    # comparator's weights are themselves rounded)
+    ref = (x.double() * step.double().cuda()) @ torch.from_numpy(codes).cuda().double().t()
+    got = ms[0].gemv(x).double()
     err = float((got - ref).norm() / ref.norm())
     out = dict(rows=rows, cols=cols, bits_target=bits, dist=dist, escape_frac=escape_frac,
                batch=batch, R=R, C=C, S=S, word_fetch={1: "always", 2: "refill"}[flags & 3],
@@ -293,7 +341,7 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
                t_rans_us=t_rans, t_bf16_us=t_bf16,
                effective_GBps=rows * cols * 2 / t_rans / 1e3,
                compressed_GBps=m.nbytes / t_rans / 1e3,
-               speedup_vs_bf16=t_bf16 / t_rans, rel_l2_vs_bf16_fp32=err, copies=ncopy)
+               speedup_vs_bf16=t_bf16 / t_rans, rel_l2_vs_f64=err, copies=ncopy)
     del ms, Ws
     torch.cuda.empty_cache()
     return out
@@ -456,6 +504,14 @@ def configs():
         r["case"] = name
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}),
               flush=True)
+    # ECSQ-GPTQ + waterfilling code statistics (the k projection's codes of a
+    # synthetic layer, tiled to the q/k/v group's shape) with their own steps
+    codes, step = ecsq_fixture(rows=2048)
+    r = config_matrix(2048, 1536, 3.25, "ecsq_wf", 0.0, 1, seed=0, lib=lib, codes=codes,
+                      step=step)
+    r["case"] = "q/k/v 2048x1536 ECSQ-GPTQ+WF codes 3.25b (k slice x8)"
+    print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}),
+          flush=True)
     for grouped in (False, True):
         r = chain(grouped=grouped)
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}),
