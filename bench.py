@@ -298,10 +298,12 @@ def main():
         return
 
     if args.sweep:
+        # tilings of the headline shape, plus the reference's published one
+        # (R=8, C=8960, mapped by encode to 8x4480 tiles with two states per lane)
         for S in (1, 2):
-            for R in (1, 2, 4, 8):
+            for R in (1, 2, 3, 4, 8):
                 for C in (640, 1280, 1792, 2240, 4480):
-                    if C % (64 * S) or COLS % C:
+                    if C % (64 * S) or COLS % C or (R * C) // (64 * S) > rans.MAX_STATE_SYMBOLS:
                         continue
                     try:
                         enc, comp, alg, ncopy, t_rot, t_hot = measure(R, C, S, 100)
