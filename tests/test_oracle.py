@@ -103,12 +103,10 @@ def _entropy_bincount(codes):
 
 
 def _record_params():
-    out = []
-    for r in _records():
-        big = r["rows"] * r["cols"] > 14_000_000  # larger than the 1536x8960 metric shape
-        out.append(pytest.param(r, id=f"{r['rows']}x{r['cols']}@{r['target_bits']}",
-                                marks=[pytest.mark.slow] if big else []))
-    return out
+    # all 18 records at full size (about 90 s on 8 cores, the 178M-weight
+    # shape 13-18 s each)
+    return [pytest.param(r, id=f"{r['rows']}x{r['cols']}@{r['target_bits']}")
+            for r in _records()]
 
 
 @pytest.mark.parametrize("rec", _record_params())
