@@ -101,7 +101,10 @@ extern "C" {
                                  RANS_EARG) and S = 1 (else RANS_EUNSUPPORTED) */
 
 typedef struct rans_w64_matrix {
-    int32_t rows, cols;       /* out_features, in_features */
+    int32_t rows, cols;       /* out_features, and the stored columns: in_features,
+                                 or in_features + 32 when in_features is an odd
+                                 multiple of 32 (x rows then hold cols values, the
+                                 last 32 zero; step's last 32 are zero) */
     int32_t R, C, S;          /* tile rows, tile columns, states per lane */
     int32_t max_tile_words;   /* largest tile block, in 16-bit words */
     int32_t max_state_words;  /* longest state stream (to the next state's start, the

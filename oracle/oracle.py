@@ -262,7 +262,10 @@ def w64_decode(enc):
     state, then the inverse layout permutation, then the escape side table.
     Raises AssertionError on a stream that does not end in state 2^16."""
     lib = load()
-    rows, cols = enc["shape"]
+    rows, ocols = enc["shape"]
+    # the stream's columns: the matrix's own plus any appended to reach a
+    # multiple of 64 (dropped from the result)
+    cols = int(enc.get("stream_cols", ocols))
     # the w64 tiling (tile_R, tile_C); R and C of the dict are the tiling the
     # encoder was asked for, which it may have mapped to another tile
     R, C, S = enc.get("tile_R", enc["R"]), enc.get("tile_C", enc["C"]), enc["S"]
@@ -306,7 +309,7 @@ def w64_decode(enc):
     if not np.array_equal(flagged, esc_mask):
         raise AssertionError("escape side table disagrees with escape symbols in the stream")
     codes[er, ec] = eval_
-    return codes
+    return codes[:, :ocols]
 
 
 # ---------------------------------------------------------------- gemv

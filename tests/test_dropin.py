@@ -46,17 +46,24 @@ def _check_enc(rans, enc, codes, R, C):
         assert k in enc, k
     assert (enc["R"], enc["C"], tuple(enc["shape"])) == (R, C, (rows, cols))
     tR, tC, tS = rans.tiling_of(enc)
+    # the stored width: cols, or cols + 32 when cols is an odd multiple of 32
+    scols = rans.stream_cols(enc)
+    assert scols == cols + (32 if cols % 64 else 0)
     # the mapped tile: a compiled height dividing R, a multiple of 64 within
     # one (or, for C % 64 == 32, two) of the reference's tiles
     assert R % tR == 0 and tR in rans.SUPPORTED_R
-    assert tC % (64 * tS) == 0 and cols % tC == 0 and (C if C % 64 == 0 else 2 * C) % tC == 0
+    assert tC % (64 * tS) == 0 and scols % tC == 0
+    if scols == cols:
+        assert (C if C % 64 == 0 else 2 * C) % tC == 0
+    else:
+        assert tC <= 2 * C
     assert tR * tC <= 65536 and tR * tC // (64 * tS) <= rans.MAX_STATE_SYMBOLS
     # offs: one word offset per state (the reference's per-lane offs), each
     # at its state's stream, which holds slen words, in state order
-    nstates = (rows // tR) * (cols // tC) * 64 * tS
+    nstates = (rows // tR) * (scols // tC) * 64 * tS
     assert enc["offs"].dtype == np.uint32 and enc["offs"].size == nstates
     ends = enc["offs"].astype(np.int64) + enc["slen"]
-    ntiles = (rows // tR) * (cols // tC)
+    ntiles = (rows // tR) * (scols // tC)
     per_tile = ends.reshape(ntiles, -1)
     starts = enc["offs"].astype(np.int64).reshape(ntiles, -1)
     np.testing.assert_array_equal(starts[:, 1:], per_tile[:, :-1])
@@ -108,6 +115,60 @@ def test_published_tilings_map(rans):
                                 (25600, 5120, 16, 640, 1), (1536, 8960, 8, 1792, 2),
                                 (1536, 8960, 16, 2240, 1)):
         assert rans.w64_tiling(rows, cols, R, C, S) == (R, C, S)
+
+
+# cols an odd multiple of 32, which the reference accepts (kernel/rans.py:57
+# asks only C % 32 == 0): (rows, cols, [C...])
+ODD32 = [(64, 96, (32, 96)), (32, 160, (32, 160)), (48, 224, (32, 224)), (70, 96, (32, 96)),
+         (6, 32, (32,)), (512, 2080, (32, 416, 2080))]
+
+
+@pytest.mark.parametrize("case", ODD32, ids=lambda c: f"{c[0]}x{c[1]}")
+def test_odd_multiple_of_32_columns(rans, oracle, case):
+    """Every (R, C) the reference accepts on a matrix whose cols is an odd
+    multiple of 32: stored with 32 appended columns of code 0 and decoded
+    back to the matrix's own shape by the product's and the oracle's
+    decoders; escapes included.  The bit accounting is per weight of the
+    matrix, and the model entropy over its own codes."""
+    rows, cols, Cs = case
+    codes = _codes(rows, cols, seed=rows * cols)
+    codes[::7, ::5] = 300  # escapes
+    for R in [r for r in range(1, rows + 1) if rows % r == 0][:6]:
+        for C in Cs:
+            enc = rans.encode(codes, R, C)
+            _check_enc(rans, enc, codes, R, C)
+            np.testing.assert_array_equal(oracle.w64_decode(enc), codes)
+    enc = rans.encode(codes, 1, Cs[0])
+    assert enc["bits_table"] == pytest.approx(32 * 4096 / codes.size)
+    # entropy_model: the matrix's own symbols under the stored table (fit to
+    # them plus the appended zeros), a cross-entropy: at least their
+    # empirical entropy (Gibbs), and close to the cross-entropy under the
+    # unquantised mixture
+    sym = np.where(np.abs(codes) <= 127, codes + 128, 0)
+    n = np.bincount(sym.ravel(), minlength=256).astype(np.float64)
+    p = n / codes.size
+    q = n.copy()
+    q[128] += rows * 32
+    q /= q.sum()
+    h = float(-(p[p > 0] * np.log2(p[p > 0])).sum())
+    x = float(-(p[p > 0] * np.log2(q[p > 0])).sum())
+    assert h - 1e-9 <= enc["entropy_model"], (h, enc["entropy_model"])
+    assert abs(enc["entropy_model"] - x) < 0.02, (x, enc["entropy_model"])
+
+
+def test_odd_multiple_of_32_container(rans, tmp_path):
+    """A matrix stored with appended columns keeps its own shape and step
+    through the container; the record's stored width is cols + 32."""
+    import rans_io
+    codes = _codes(96, 160, seed=3)
+    step = np.linspace(0.5, 1.5, 160).astype(np.float32)
+    enc = rans.encode(codes, 8, 32)
+    path = str(tmp_path / "odd.w64")
+    rans_io.save(path, [dict(name="m", enc=enc, step=step)])
+    e = rans_io.load(path)[0]
+    assert tuple(e["enc"]["shape"]) == (96, 160) and rans.stream_cols(e["enc"]) == 192
+    np.testing.assert_array_equal(e["step"], step)
+    np.testing.assert_array_equal(rans.decode_ref(e["enc"]), codes)
 
 
 def test_reference_entry_points_refuse(rans):

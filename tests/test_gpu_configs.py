@@ -79,6 +79,35 @@ def test_reference_tilings(rans, oracle, lib, dev, case):
     _check(rans, oracle, lib, codes, R, C, step, x, x_bf16=True)
 
 
+@pytest.mark.parametrize("case", [(64, 96, 1, 32, True), (70, 96, 35, 96, True),
+                                  (512, 2080, 16, 32, False), (2048, 1568, 8, 1568, True)],
+                         ids=lambda c: "x".join(map(str, c[:4])))
+def test_odd_multiple_of_32_columns(rans, oracle, lib, dev, case):
+    """cols an odd multiple of 32 (the reference needs only C % 32 == 0,
+    kernel/rans.py:57): stored with 32 appended columns, whose zero step and
+    zero-padded x add nothing.  Decode paths bit-exact at the matrix's own
+    shape; GEMV at batch 1 and 4 within the bar of the oracle; a grouped
+    launch of two such matrices bitwise their single launches.  1% escapes."""
+    import rans_bench as B
+    rows, cols, R, C, xbf = case
+    print(f"case odd-32 columns {case}", flush=True)
+    codes = B.synth_codes_full(rows, cols, 3.25, seed=rows + cols, escape_frac=0.01)
+    step = B.lognormal_steps(cols, seed=cols)
+    x = np.random.default_rng(3).standard_normal(cols).astype(np.float32)
+    m, _, _ = _check(rans, oracle, lib, codes, R, C, step, x, x_bf16=xbf)
+    assert m.stream_cols == cols + 32
+    xb = torch.randn(4, cols, device="cuda")
+    xb = xb.bfloat16() if xbf else xb
+    y4 = m.gemv(xb).cpu().numpy()
+    ref4 = oracle.gemv_f64(codes, xb.float().cpu().numpy().astype(np.float64),
+                           step.astype(np.float64))
+    assert _rel_l2(y4, ref4) <= REL_L2
+    codes2 = B.synth_codes_full(rows, cols, 3.25, seed=rows + cols + 1, escape_frac=0.01)
+    m2 = rans.RansMatrix(rans.encode(codes2, R, C), torch.from_numpy(step), lib)
+    ys = rans.gemv_group([m, m2], xb)
+    assert torch.equal(ys[0], m.gemv(xb)) and torch.equal(ys[1], m2.gemv(xb))
+
+
 CHAIN_LAYERS = int(os.environ.get("CHAIN_TEST_LAYERS", "28"))
 
 

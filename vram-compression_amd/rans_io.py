@@ -19,18 +19,20 @@ Layout (all integers little endian, every section 64-byte aligned):
     index, nmat records of 256 bytes
         name       64 bytes UTF-8, NUL padded
         rows, cols, R, C, S, max_tile_words, max_state_words, flags   i32 x 8
-                   (R, C, S: the w64 tiling, tile_R/tile_C/S of the enc dict)
+                   (cols: the stored columns, stream_cols of the enc dict;
+                   R, C, S: the w64 tiling, tile_R/tile_C/S of the enc dict)
         nwords, ntiles, nstates, nesc, payload_words                  u64 x 5
         entropy_model                                                 f64
         offsets of words, tile_off, slen, states, table, esc_tileptr,
                    esc_pos, esc_val, step                             u64 x 9
         crc32 of the nine sections, in that order                     u32
+        appended columns (0, or 32 when the matrix's cols % 64 == 32)  i32
         zero padding to 256 bytes
     sections
         words u16[nwords], tile_off u32[ntiles+1], slen u8[nstates],
         states u32[nstates], table u32[4096] (reference packing),
         esc_tileptr i32[ntiles+1], esc_pos u16[nesc], esc_val i16[nesc],
-        step f32[cols]
+        step f32[cols - appended columns]
 
 `flags` holds the launch options chosen for the matrix (the RANS_F_* word
 fetch and table-entry bits; 0 = library defaults), so a tuned set reloads
@@ -47,7 +49,7 @@ import rans
 MAGIC = b"VRAMCW64"
 VERSION = 4
 _HEADER = struct.Struct("<8sIIQQ32x")
-_RECORD = struct.Struct("<64s8i5Qd9QI")
+_RECORD = struct.Struct("<64s8i5Qd9QIi")
 RECORD_BYTES = 256
 ALIGN = 64
 _SECTIONS = (("words", np.uint16), ("tile_off", np.uint32), ("slen", np.uint8),
@@ -60,7 +62,8 @@ def _align(n):
     return (n + ALIGN - 1) // ALIGN * ALIGN
 
 
-def _section_lengths(rows, cols, nwords, ntiles, nstates, nesc):
+def _section_lengths(cols, nwords, ntiles, nstates, nesc):
+    """Entries of each section; cols: the matrix's own columns (step)."""
     return dict(words=nwords, tile_off=ntiles + 1, slen=nstates, states=nstates,
                 table=rans.M, esc_tileptr=ntiles + 1, esc_pos=nesc, esc_val=nesc, step=cols)
 
@@ -75,11 +78,12 @@ def save(path, entries):
     for e in entries:
         enc = e["enc"]
         rows, cols = (int(v) for v in enc["shape"])
+        scols = rans.stream_cols(enc)
         arrays = {}
         for key, dt in _SECTIONS:
             a = e["step"] if key == "step" else enc[key]
             arrays[key] = np.ascontiguousarray(np.asarray(a).reshape(-1), dtype=dt)
-        n = _section_lengths(rows, cols, arrays["words"].size, arrays["tile_off"].size - 1,
+        n = _section_lengths(cols, arrays["words"].size, arrays["tile_off"].size - 1,
                              arrays["states"].size, arrays["esc_pos"].size)
         for key, _ in _SECTIONS:
             assert arrays[key].size == n[key], f"{e['name']}: {key} has {arrays[key].size} " \
@@ -94,12 +98,13 @@ def save(path, entries):
             pos = _align(pos + len(b))
         name = e["name"].encode("utf-8")
         assert len(name) <= 64, "matrix names are at most 64 bytes of UTF-8"
-        recs.append(_RECORD.pack(name, rows, cols, *rans.tiling_of(enc),
+        recs.append(_RECORD.pack(name, rows, scols, *rans.tiling_of(enc),
                                  enc["max_tile_words"], enc["max_state_words"],
                                  int(e.get("flags", 0)), arrays["words"].size,
                                  arrays["tile_off"].size - 1, arrays["states"].size,
                                  arrays["esc_pos"].size, payload_words,
-                                 float(enc.get("entropy_model", 0.0)), *offs, crc))
+                                 float(enc.get("entropy_model", 0.0)), *offs, crc,
+                                 scols - cols))
     total = pos
     tmp = f"{path}.tmp{os.getpid()}"
     with open(tmp, "wb") as f:
@@ -148,11 +153,13 @@ def load(path, verify=True, mmap=True):
         entropy_model = v[14]
         offs = v[15:24]
         crc_want = v[24]
+        appended = v[25]
         if rows <= 0 or cols <= 0 or R <= 0 or C <= 0 or S <= 0 or rows % R or cols % C \
                 or C % (64 * S) or ntiles != (rows // R) * (cols // C) \
-                or nstates != ntiles * 64 * S:
+                or nstates != ntiles * 64 * S or appended not in (0, 32):
             raise ValueError(f"{name}: inconsistent geometry in the index")
-        n = _section_lengths(rows, cols, nwords, ntiles, nstates, nesc)
+        scols, cols = cols, cols - appended
+        n = _section_lengths(cols, nwords, ntiles, nstates, nesc)
         arrays, crc = {}, 0
         for (key, dt), off in zip(_SECTIONS, offs):
             nbytes = n[key] * np.dtype(dt).itemsize
@@ -170,7 +177,7 @@ def load(path, verify=True, mmap=True):
                    states=arrays["states"], table=arrays["table"],
                    esc_tileptr=arrays["esc_tileptr"], esc_pos=arrays["esc_pos"],
                    esc_val=arrays["esc_val"], R=R, C=C, tile_R=R, tile_C=C, S=S,
-                   shape=(rows, cols),
+                   shape=(rows, cols), stream_cols=scols,
                    max_tile_words=mtw, max_state_words=msw,
                    bits_payload=16 * payload_words / N,
                    bits_state_offs=(40 * nstates + 32 * (ntiles + 1) + 16 * pad) / N,
