@@ -108,6 +108,21 @@ def test_odd_multiple_of_32_columns(rans, oracle, lib, dev, case):
     assert torch.equal(ys[0], m.gemv(xb)) and torch.equal(ys[1], m2.gemv(xb))
 
 
+def test_scalar_step_broadcasts(rans, lib, dev):
+    """A one-value step (a per-tensor scale) acts as that value in every
+    column, as the reference's x * step broadcast would: bitwise the same
+    GEMV and decode as the explicit per-column vector."""
+    import rans_bench as B
+    print("case scalar step 256x512", flush=True)
+    codes = B.synth_codes_full(256, 512, 3.25, seed=7)
+    enc = rans.encode(codes, 8, 512)
+    a = rans.RansMatrix(enc, torch.tensor(0.0123), lib)
+    b = rans.RansMatrix(enc, torch.full((512,), 0.0123), lib)
+    x = torch.randn(3, 512, device="cuda").bfloat16()
+    assert torch.equal(a.gemv(x), b.gemv(x))
+    assert torch.equal(a.decode(), b.decode())
+
+
 CHAIN_LAYERS = int(os.environ.get("CHAIN_TEST_LAYERS", "28"))
 
 
