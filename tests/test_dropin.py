@@ -181,3 +181,30 @@ def test_reference_entry_points_refuse(rans):
         fn.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
         fn.restype = ctypes.c_int
         assert fn(8, 1, 2, 3, 4, 5, 1536, 8960, 8960, None) == -1
+
+
+def test_random_reference_tilings(rans, oracle):
+    """Property test over the reference's preconditions: any R, any C with
+    C % 32 == 0, rows = a*R and cols = b*C (odd multiples of 32 included),
+    codes from narrow to wide (escapes up to the 16-bit limits).  encode
+    accepts each, and both decoders give the codes back."""
+    from hypothesis import given, settings, strategies as st
+
+    @settings(max_examples=60, deadline=None, derandomize=True)
+    @given(R=st.integers(1, 40), a=st.integers(1, 3), k=st.integers(1, 12),
+           b=st.integers(1, 3), scale=st.floats(0.3, 40.0), esc=st.sampled_from([0.0, 0.01, 0.2]),
+           seed=st.integers(0, 2**31 - 1))
+    def prop(R, a, k, b, scale, esc, seed):
+        C = 32 * k
+        rows, cols = a * R, b * C
+        rng = np.random.default_rng(seed)
+        codes = np.clip(np.round(rng.laplace(size=(rows, cols)) * scale), -127, 127).astype(np.int64)
+        mask = rng.random(codes.shape) < esc
+        codes[mask] = rng.choice([-32768, -200, 128, 32767], size=int(mask.sum()))
+        if np.unique(codes).size < 2:
+            codes.flat[0] = codes.flat[0] + 1
+        enc = rans.encode(codes, R, C)
+        _check_enc(rans, enc, codes, R, C)
+        np.testing.assert_array_equal(oracle.w64_decode(enc), codes)
+
+    prop()
