@@ -231,6 +231,8 @@ def main():
                     help="skip the per-token chain (196 GEMVs, grouped launches)")
     ap.add_argument("--no-ecsq", action="store_true",
                     help="skip the row with ECSQ-GPTQ + waterfilling code statistics")
+    ap.add_argument("--no-reflayout", action="store_true",
+                    help="skip the reference's own 32-lane layout at its published tiling")
     ap.add_argument("--sweep", action="store_true", help="print a tiling sweep to stderr")
     ap.add_argument("--profile", action="store_true",
                     help="for rocprofv3: K eager launches of the headline GEMV over the rotating "
@@ -352,6 +354,31 @@ def main():
         print(f"bf16 F.linear: {tb_rot:.2f} us rotated, {tb_hot:.2f} us hot", file=sys.stderr,
               flush=True)
 
+    # The same matrix in the reference's own 32-lane layout at its published
+    # tiling of this shape (R=8, C=8960: 6144 streams of 2240 symbols,
+    # results/kernel_bench.json:128-129), through the reference's entry point
+    # launch_rans_gemv with the host fold, rotated the same way.
+    reflayout = None
+    if not args.no_reflayout:
+        renc = rans.encode_reference_layout(codes, 8, COLS)
+        rm0 = rans.ReferenceLayoutMatrix(renc, step_t, lib)
+        nr = copies_for(args.steps, rm0.nbytes)
+        rms = [rm0] + [rans.ReferenceLayoutMatrix(renc, step_t, lib) for _ in range(nr - 1)]
+        yr = torch.empty(ROWS, device="cuda")
+        rfns = [lambda rm=rm: rm.gemv(xb, yr) for rm in rms]
+        tr_rot = graph_time_us(rfns, args.steps, args.warmup, rotate=nr)
+        tr_hot = graph_time_us(rfns[:1], args.steps, args.warmup)
+        reflayout = {"R": 8, "C": COLS, "streams": int(renc["offs"].size),
+                     "bits_total": 8 * rm0.nbytes / codes.size,
+                     "us_per_gemv": tr_rot, "hot_us_per_gemv": tr_hot, "copies": nr,
+                     "w64_speedup": tr_rot / t_rot,
+                     "note": "host fold x*step plus launch_rans_gemv, as the reference's "
+                             "RansMatrix.gemv does"}
+        del rms, rm0, rfns
+        torch.cuda.empty_cache()
+        print(f"reference layout R=8 C={COLS}: {tr_rot:.2f} us rotated, {tr_hot:.2f} us hot",
+              file=sys.stderr, flush=True)
+
     cpu = None if args.no_cpu else cpu_baseline(codes, step, torch.from_numpy(x).bfloat16().float().numpy())
 
     # The per-token chain of a Qwen2.5-1.5B-shaped weight set (28 layers x 7
@@ -413,6 +440,7 @@ def main():
         "hot_effective_GBps": ROWS * COLS * 2 / t_hot / 1e3,
         "compressed_GBps": comp / t_rot / 1e3,
         "rocblas_bf16": rocblas,
+        "reference_layout": reflayout,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "traffic_source": None if traffic is None else

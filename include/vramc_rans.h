@@ -200,14 +200,20 @@ int rans_w64_decode_codes(const rans_w64_matrix* m, int32_t* out, hipStream_t st
 int launch_int4_gemv(const void* w, const void* x, void* y, int rows, int cols,
                      hipStream_t stream);
 
-/* The reference's two rANS entry points, with its argument lists
- * (rans_gemv.cu:146-162, bound by kernel/rans.py:25-29 as
- * [c_int] + [c_void_p]*5 + [c_int]*3 + [c_void_p]).  They take the
- * reference's 32-lane stream (words, offs), which this library does not
- * decode on the GPU: both return RANS_EUNSUPPORTED and launch nothing, so a
- * binding written for the reference gets the reference's own "unsupported"
- * code instead of a crash.  The w64 format is launched with rans_w64_gemv and
- * rans_w64_decode. */
+/* The reference's two rANS entry points, with its argument lists and stream
+ * format (rans_gemv.cu:146-162, bound by kernel/rans.py:25-29 as
+ * [c_int] + [c_void_p]*5 + [c_int]*3 + [c_void_p]): words / offs / table as
+ * the reference's encode returns them (kernel/rans.py:62-98, 32-lane tiles of
+ * R x C, R in {1, 2, 4, 8, 16}, C % 32 == 0, codes in [-128, 127]).
+ * launch_rans_gemv: y[r] = sum_c code[r,c] * x[c] for the host-folded f32
+ * x = x*step, written when cols == C, else added into y, which the caller
+ * zeroes (rans.py:141-146).  launch_rans_decode: out[r,c] = bf16(code[r,c] *
+ * step[c]).  Another R returns RANS_EUNSUPPORTED (-1, the reference's own
+ * code) before anything is touched; RANS_EARG / RANS_EGEOMETRY for null
+ * pointers or a shape that does not divide.  `words` must be device memory of
+ * one allocation (hipMemGetAddressRange finds its end; no read goes past
+ * it).  The format's streams are few and long, so this is the compatibility
+ * path: rans_w64_gemv on the w64 layout is the fast one. */
 int launch_rans_gemv(int R, const void* words, const void* offs, const void* table,
                      const void* x, void* y, int rows, int cols, int C, hipStream_t stream);
 int launch_rans_decode(int R, const void* words, const void* offs, const void* table,
@@ -264,6 +270,17 @@ void rans_w64_encode_free(void* handle);
  * rans.py:121), RANS_EARG on a stream overrun or an escape side table that
  * disagrees with the escape symbols in the stream. */
 int rans_w64_decode_host(const rans_w64_matrix* m_host, int32_t* out);
+
+/* The reference's encoder for its own 32-lane layout (kernel/rans.py:62-98),
+ * the input of launch_rans_gemv / launch_rans_decode: codes (rows x cols,
+ * int32 in [-128, 127], else RANS_ECODES) in R x C tiles (C % 32 == 0);
+ * writes words (capacity words_cap >= 2*lanes + rows*cols + 8, lanes =
+ * 32*(rows/R)*(cols/C)), offs[lanes] and table[4096] exactly as the
+ * reference's encode lays them out, and info[0] = words used (with the 8
+ * trailing zero words), info[1] = renormalisation words.  Host only. */
+int rans_ref32_encode(const int32_t* codes, int32_t rows, int32_t cols, int32_t R, int32_t C,
+                      int32_t nthreads, uint16_t* words, int64_t words_cap, uint32_t* offs,
+                      uint32_t* table, int64_t* info);
 
 #ifdef __cplusplus
 }

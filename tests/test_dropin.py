@@ -171,16 +171,25 @@ def test_odd_multiple_of_32_container(rans, tmp_path):
     np.testing.assert_array_equal(rans.decode_ref(e["enc"]), codes)
 
 
-def test_reference_entry_points_refuse(rans):
+def test_reference_entry_points_check_arguments(rans):
     """The reference's launch_rans_gemv / launch_rans_decode argument lists
-    (kernel/rans.py:25-29) reach entry points that return the reference's
-    "unsupported" code (-1) and touch nothing, instead of crashing."""
+    (kernel/rans.py:25-29) reach entry points that check them before any
+    device call: an R the reference has no kernel for returns its own -1
+    (rans_gemv.cu:137-144), a null pointer RANS_EARG, a shape that does not
+    divide RANS_EGEOMETRY.  (Decoding the reference's streams is tested on
+    the GPU.)"""
     lib = ctypes.CDLL(rans.LIB)
     for name in ("launch_rans_gemv", "launch_rans_decode"):
         fn = getattr(lib, name)
         fn.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
         fn.restype = ctypes.c_int
-        assert fn(8, 1, 2, 3, 4, 5, 1536, 8960, 8960, None) == -1
+        for R in (3, 512, 0, -8):
+            assert fn(R, 1, 2, 3, 4, 5, 1536, 8960, 8960, None) == -1
+        assert fn(8, None, 2, 3, 4, 5, 1536, 8960, 8960, None) == -4
+        assert fn(8, 1, 2, 3, 4, None, 1536, 8960, 8960, None) == -4
+        assert fn(8, 1, 2, 3, 4, 5, 1536, 8960, 8976, None) == -2  # C does not divide cols
+        assert fn(8, 1, 2, 3, 4, 5, 1536, 8960, 8944, None) == -2  # C % 32
+        assert fn(16, 1, 2, 3, 4, 5, 1544, 8960, 8960, None) == -2  # R does not divide rows
 
 
 def test_random_reference_tilings(rans, oracle):
@@ -208,3 +217,40 @@ def test_random_reference_tilings(rans, oracle):
         np.testing.assert_array_equal(oracle.w64_decode(enc), codes)
 
     prop()
+
+
+@pytest.mark.parametrize("i", range(4))
+def test_reference_layout_encoder_matches_reference(rans, golden, i):
+    """encode_reference_layout writes the reference's own encode output
+    (kernel/rans.py:62-98) for its test shapes byte for byte: words (with
+    the 8 trailing words), offs, table and the bit accounting."""
+    rows, cols, R, C = (int(v) for v in golden[f"enc{i}_meta"])
+    codes = golden[f"enc{i}_codes"].astype(np.int32)
+    enc = rans.encode_reference_layout(codes, R, C)
+    np.testing.assert_array_equal(enc["words"], golden[f"enc{i}_words"])
+    np.testing.assert_array_equal(enc["offs"], golden[f"enc{i}_offs"])
+    np.testing.assert_array_equal(enc["table"], golden[f"enc{i}_table"])
+    bits = golden[f"enc{i}_bits"]
+    assert enc["bits_payload"] == bits[1] and enc["bits_state_offs"] == bits[2]
+    assert enc["bits_table"] == bits[3]
+    assert abs(enc["entropy_model"] - bits[4]) < 1e-12
+    assert (enc["R"], enc["C"], tuple(enc["shape"])) == (R, C, (rows, cols))
+
+
+@pytest.mark.parametrize("case", [(1536, 8960, 8, 8960, 3.25), (96, 1536, 4, 512, 4.25),
+                                  (48, 768, 16, 256, 2.25), (32, 64, 1, 32, 1.0)],
+                         ids=lambda c: "x".join(map(str, c[:4])))
+def test_reference_layout_encoder_matches_oracle(rans, oracle, case):
+    """Larger shapes against the oracle's restatement of the reference's
+    encoder, any thread count; codes at both ends of the 8-bit alphabet."""
+    rows, cols, R, C, bits = case
+    codes = oracle.synth_codes(rows, cols, bits, seed=rows + cols).astype(np.int32)
+    codes[0, :2] = (-128, 127)
+    want = oracle.encode_ref(codes, R, C)
+    for threads in (1, 5):
+        enc = rans.encode_reference_layout(codes, R, C, threads=threads)
+        for k in ("words", "offs", "table"):
+            np.testing.assert_array_equal(enc[k], want[k])
+        assert enc["bits_payload"] == want["bits_payload"]
+    with pytest.raises(AssertionError):
+        rans.encode_reference_layout(np.where(codes == 127, 128, codes), R, C)

@@ -1467,16 +1467,6 @@ extern "C" int rans_gemv_rows2(const rans_w64_matrix* m, int x_dtype, int batch)
     return 0;
 }
 
-extern "C" int launch_rans_gemv(int, const void*, const void*, const void*, const void*, void*,
-                                int, int, int, hipStream_t) {
-    return RANS_EUNSUPPORTED;
-}
-
-extern "C" int launch_rans_decode(int, const void*, const void*, const void*, const void*, void*,
-                                  int, int, int, hipStream_t) {
-    return RANS_EUNSUPPORTED;
-}
-
 extern "C" int rans_w64_decode(const rans_w64_matrix* m, void* out_bf16, hipStream_t stream) {
     return launch_decode_common<1>(m, out_bf16, stream);
 }

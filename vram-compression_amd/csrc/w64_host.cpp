@@ -403,3 +403,69 @@ extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
     }
     return 0;
 }
+
+// The reference's own 32-lane layout (kernel/rans.py:55-98), for the
+// reference-format entry points (launch_rans_gemv / launch_rans_decode): one
+// stream per lane of 32-column tiles, lanes in tile order, each stream its
+// final encoder state as two words and then its renormalisation words in
+// decode order, 8 zero words after the last stream.  The table is built with
+// the same quantisation as the w64 encoder, from symbols code + 128 (codes in
+// [-128, 127], no escapes).  Lanes are encoded on up to nthreads threads; the
+// output does not depend on the thread count.
+extern "C" int rans_ref32_encode(const int32_t* codes, int32_t rows, int32_t cols, int32_t R,
+                                 int32_t C, int32_t nthreads, uint16_t* words, int64_t words_cap,
+                                 uint32_t* offs, uint32_t* table, int64_t* info) {
+    if (!codes || !words || !offs || !table || !info || rows <= 0 || cols <= 0 || R <= 0 ||
+        C <= 0)
+        return RANS_EARG;
+    if (rows % R || cols % C || C % 32) return RANS_EGEOMETRY;
+    const int64_t N = (int64_t)rows * cols;
+    const int32_t ncb = cols / C;
+    const int64_t lanes = (int64_t)(rows / R) * ncb * 32;
+    const int64_t n = (int64_t)(C / 32) * R;  // symbols per lane
+    if (words_cap < 2 * lanes + N + 8) return RANS_EARG;  // the longest possible output
+    int64_t counts[256] = {0};
+    for (int64_t i = 0; i < N; i++) {
+        const int32_t v = codes[i];
+        if (v < -128 || v > 127) return RANS_ECODES;
+        counts[v + 128]++;
+    }
+    int64_t freq[256], cum[256];
+    if (table_from_counts(counts, N, freq, cum, table) != 0) return RANS_ECODES;
+
+    // each lane's emitted words (in encode order) and final state
+    std::vector<std::vector<uint16_t>> emitted((size_t)lanes);
+    std::vector<uint32_t> final_state((size_t)lanes);
+    const int nth = nthreads > 0 ? nthreads : 1;
+    parallel_for(lanes, nth, [&](int64_t li) {
+        const int64_t t = li / 32, l = li % 32;
+        const int64_t rb = t / ncb, cb = t % ncb;
+        std::vector<uint16_t>& out = emitted[(size_t)li];
+        out.reserve((size_t)(n / 2 + 4));
+        uint64_t x = kRansL;
+        for (int64_t i = n - 1; i >= 0; i--) {
+            const int64_t k = i / R, r = i % R;  // symbol i = k*R + r
+            const int32_t s = codes[(rb * R + r) * cols + cb * C + 32 * k + l] + 128;
+            const uint64_t f = (uint64_t)freq[s], c = (uint64_t)cum[s];
+            if (x >= ((uint64_t)1 << 20) * f) {
+                out.push_back((uint16_t)(x & 0xFFFFu));
+                x >>= 16;
+            }
+            x = ((x / f) << kScaleBits) + x % f + c;
+        }
+        final_state[(size_t)li] = (uint32_t)x;
+    });
+    int64_t pos = 0, payload = 0;
+    for (int64_t li = 0; li < lanes; li++) {
+        const std::vector<uint16_t>& out = emitted[(size_t)li];
+        offs[li] = (uint32_t)pos;
+        words[pos++] = (uint16_t)(final_state[(size_t)li] >> 16);
+        words[pos++] = (uint16_t)(final_state[(size_t)li] & 0xFFFFu);
+        for (size_t j = out.size(); j-- > 0;) words[pos++] = out[j];
+        payload += (int64_t)out.size();
+    }
+    for (int j = 0; j < 8; j++) words[pos++] = 0;
+    info[0] = pos;
+    info[1] = payload;
+    return 0;
+}
