@@ -164,3 +164,34 @@ def test_reference_layout_matrix(rans, oracle, lib, dev):
                                     torch.tensor(0.02), lib)
     want = (torch.from_numpy(codes[:64, :512].astype(np.float32)) * 0.02).bfloat16()
     assert torch.equal(m1.decode().cpu().view(torch.int16), want.view(torch.int16))
+
+
+def test_reference_format_exact_size_allocation(rans, lib, golden, dev):
+    """`words` in an allocation of exactly its own size (hipMalloc of 3849
+    words, not a whole number of 16-byte chunks): the last wave's span is cut
+    at the allocation's end and its last words are staged one by one; the
+    decode is still exact."""
+    import ctypes
+    rows, cols, R, C = (int(v) for v in golden["enc0_meta"])
+    words = np.ascontiguousarray(golden["enc0_words"])
+    assert words.nbytes % 16
+    hip = ctypes.CDLL("libamdhip64.so")
+    ptr = ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(ptr), ctypes.c_size_t(words.nbytes)) == 0
+    try:
+        assert hip.hipMemcpy(ptr, words.ctypes.data_as(ctypes.c_void_p),
+                             ctypes.c_size_t(words.nbytes), 1) == 0  # host to device
+        offs = torch.from_numpy(golden["enc0_offs"].view(np.int32)).cuda()
+        table = torch.from_numpy(golden["enc0_table"].view(np.int32)).cuda()
+        step = torch.full((cols,), 0.5, device="cuda")
+        out = torch.full((rows, cols), float("nan"), device="cuda", dtype=torch.bfloat16)
+        rc = lib.launch_rans_decode(R, ptr.value, offs.data_ptr(), table.data_ptr(),
+                                    step.data_ptr(), out.data_ptr(), rows, cols, C,
+                                    torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, rc
+        torch.cuda.synchronize()
+        want = (torch.from_numpy(golden["enc0_codes"].astype(np.float32)) * 0.5).bfloat16()
+        assert torch.equal(out.cpu().view(torch.int16), want.view(torch.int16))
+    finally:
+        torch.cuda.synchronize()
+        hip.hipFree(ptr)

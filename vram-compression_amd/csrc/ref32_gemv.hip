@@ -138,35 +138,40 @@ __global__ void __launch_bounds__(64 * kRefMaxWaves) ref32_kernel(Ref32Args a) {
     uint16_t* slot = ref_dyn + (size_t)wave * a.slot;
     const int nsym = (a.C / 32) * R;
 
-    // The span of the wave's streams in 16-byte chunks [c0, c1): from its
-    // first lane's offset to the next wave's first offset, or past the last
-    // lane's longest possible stream; chunks past the allocation read as 0.
-    int64_t c0 = 0, c1 = 0;
+    // The span of the wave's streams, words [w0, w1): from its first lane's
+    // offset (rounded down to a 16-byte chunk) to the next wave's first
+    // offset, or past the last lane's longest possible stream; never past
+    // the end of the allocation.
+    int64_t w0 = 0, w1 = 0;
     if (live) {
-        c0 = (int64_t)a.offs[base] >> 3;
+        w0 = ((int64_t)a.offs[base] >> 3) << 3;
         const int64_t end = base + 64 < a.nlanes
                                 ? (int64_t)a.offs[base + 64] + 1
                                 : (int64_t)a.offs[a.nlanes - 1] + 3 + nsym;
-        c1 = (min(end, a.words_avail) + 7) >> 3;
+        w1 = min(end, a.words_avail);
     }
-    const int64_t span = (c1 - c0) * 8;
     // staged when the span (plus the read-ahead slack) fits the slot and
     // every lane's stream starts inside it (offsets in lane order, as the
     // reference's encoder writes them; otherwise the global path)
     const uint32_t p0 = active ? a.offs[L] : 0u;
-    const bool inside = !active || ((int64_t)p0 >= c0 * 8 && (int64_t)p0 < c1 * 8);
-    const bool staged = live && span + 8 <= a.slot && c1 > c0 &&
+    const bool inside = !active || ((int64_t)p0 >= w0 && (int64_t)p0 < w1);
+    const bool staged = live && w1 > w0 && (w1 - w0) + 8 <= a.slot &&
                         __builtin_amdgcn_ballot_w64(!inside) == 0;
-    const int64_t avail_bytes = (a.words_avail - c0 * 8) * 2;
-    const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(a.words) + c0 * 8, 0,
-        (int)min(max(avail_bytes, (int64_t)0), (int64_t)0x7FFFFFFF), kRefBufWord3);
     if (staged) {
-        const int n16 = (int)(c1 - c0);
-        for (int j = lane; j < n16; j += 64) {
+        // whole 16-byte chunks that end inside the allocation, then the last
+        // few words one by one: every load lies in range
+        const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(a.words) + w0, 0,
+            (int)min((a.words_avail - w0) * 2, (int64_t)0x7FFFFFFF), kRefBufWord3);
+        const int nfull = (int)min((w1 - w0 + 7) >> 3, (a.words_avail - w0) >> 3);
+        for (int j = lane; j < nfull; j += 64) {
             auto v = __builtin_amdgcn_raw_buffer_load_b128(srs, j * 16, 0, 0);
             *reinterpret_cast<decltype(v)*>(slot + 8 * j) = v;
         }
+        const int ntail = (int)(w1 - w0) - 8 * nfull;  // < 8
+        if (lane < ntail)
+            slot[8 * nfull + lane] =
+                __builtin_amdgcn_raw_buffer_load_b16(srs, (8 * nfull + lane) * 2, 0, 0);
     }
     __syncthreads();
 
@@ -187,7 +192,7 @@ __global__ void __launch_bounds__(64 * kRefMaxWaves) ref32_kernel(Ref32Args a) {
                 acc[r] = fmaf((float)code, xv, acc[r]);
         };
         if (staged) {
-            uint32_t ad = ref_lds_addr(slot + (p0 - (uint32_t)(c0 * 8)));
+            uint32_t ad = ref_lds_addr(slot + (p0 - (uint32_t)w0));
             uint32_t st = (ref_lds_u16(ad) << 16) | ref_lds_u16(ad + 2u);
             ad += 4u;
             uint32_t w = ref_lds_u16(ad);
