@@ -290,6 +290,56 @@ def bench(rotate_bytes=512 << 20, iters=200):
         json.dump(out, f, indent=1)
 
 
+def bench_reference_layout(rotate_bytes=512 << 20, iters=200, out_name="kernel_bench_reflayout.json"):
+    """bench.py:82-126 on the reference's own 32-lane layout
+    (encode_reference_layout + ReferenceLayoutMatrix, launch_rans_gemv with
+    the host fold): the same shapes, rates, record keys and (R, C) sweep,
+    the best tiling picked on hot timings as the reference's bench does,
+    then timed again over rotated copies (t_rans_us; the hot figure is
+    t_rans_hot_us).  The comparators are left out: bench() measures them on
+    the same inputs."""
+    lib = rans.build()
+    shapes = {"1.5B qkv": (2048, 1536), "1.5B gate_up": (17920, 1536), "1.5B down": (1536, 8960),
+              "27B-like attn": (5120, 5120), "27B-like gate_up": (34816, 5120),
+              "27B-like down": (5120, 17408)}
+    out = []
+    for name, (rows, cols) in shapes.items():
+        for bits in (2.0, 3.0, 4.0):
+            codes = synth_codes(rows, cols, bits, seed=rows + cols)
+            step = torch.rand(cols) * 0.01 + 0.005
+            x = torch.randn(cols, device="cuda")
+            yb = torch.empty(rows, device="cuda")
+            best = None
+            for R in (4, 8, 16):
+                for C in sorted({cols, 512, 1024, 2048} & set(range(32, cols + 1, 32))):
+                    if cols % C or rows % R:
+                        continue
+                    enc = rans.encode_reference_layout(codes, R, C)
+                    m = rans.ReferenceLayoutMatrix(enc, step, lib)
+                    t = timeit_graph(lambda: m.gemv(x, yb), iters)
+                    if best is None or t < best[0]:
+                        best = (t, R, C, enc)
+                    del m
+            t_hot, R, C, enc = best
+            m0 = rans.ReferenceLayoutMatrix(enc, step, lib)
+            ncopy = copies_for(iters, m0.nbytes, rotate_bytes)
+            ms = [m0] + [rans.ReferenceLayoutMatrix(enc, step, lib) for _ in range(ncopy - 1)]
+            t = timeit_graph([lambda mm=mm: mm.gemv(x, yb) for mm in ms], iters, rotate=True)
+            del ms
+            r = dict(shape=name, rows=rows, cols=cols, entropy=entropy_fast(codes), R=R, C=C,
+                     t_rans_us=t, t_rans_hot_us=t_hot, bits_total=8 * m0.nbytes / codes.size,
+                     bits_payload=enc["bits_payload"],
+                     bits_overhead=enc["bits_state_offs"] + enc["bits_table"], copies=ncopy)
+            del m0
+            print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}),
+                  flush=True)
+            out.append(r)
+            torch.cuda.empty_cache()
+    os.makedirs(RES, exist_ok=True)
+    with open(os.path.join(RES, out_name), "w") as f:
+        json.dump(out, f, indent=1)
+
+
 # ------------------------------------------------ benchmark configurations
 def qwen15b_layer_shapes():
     """(name, rows, cols) of one Qwen2.5-1.5B decoder layer's linear maps."""
@@ -550,5 +600,7 @@ if __name__ == "__main__":
             r = chain(layers=layers, grouped=grouped, batch=batch)
             print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
                               for k, v in r.items()}), flush=True)
+    elif sys.argv[1] == "bench" and sys.argv[2:] == ["reference"]:
+        bench_reference_layout()
     else:
         {"test": test, "bench": bench, "configs": configs}[sys.argv[1]]()
