@@ -204,10 +204,14 @@ __global__ void __launch_bounds__(64 * kRefMaxWaves) ref32_kernel(Ref32Args a) {
                 for (int r = 0; r < R; r++) emit(k, r, ref_step_lds(st, ad, w, tab), xv);
             }
         } else {
+            // ranged from the wave's first offset, so the byte offsets stay
+            // small; a lane whose offset lies below it (offsets out of lane
+            // order) reads out of range, i.e. zeros, never another buffer
             const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint16_t*>(a.words), 0,
-                (int)min(a.words_avail * 2, (int64_t)0x7FFFFFFF), kRefBufWord3);
-            uint32_t p = p0;
+                const_cast<uint16_t*>(a.words) + w0, 0,
+                (int)min(max(a.words_avail - w0, (int64_t)0) * 2, (int64_t)0x7FFFFFFF),
+                kRefBufWord3);
+            uint32_t p = p0 - (uint32_t)w0;
             uint32_t st = ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(wrs, (int)(p * 2u), 0, 0)
                            << 16) |
                           __builtin_amdgcn_raw_buffer_load_b16(wrs, (int)(p * 2u + 2u), 0, 0);
