@@ -254,3 +254,19 @@ def test_reference_layout_encoder_matches_oracle(rans, oracle, case):
         assert enc["bits_payload"] == want["bits_payload"]
     with pytest.raises(AssertionError):
         rans.encode_reference_layout(np.where(codes == 127, 128, codes), R, C)
+
+
+def test_pick_tiling_odd_multiple_of_32(rans, oracle):
+    """pick_tiling tiles an odd multiple of 32 columns over its stored width,
+    and encode takes that tile width (a multiple of 64 dividing the stored
+    columns) as it is."""
+    for rows, cols in ((64, 96), (1536, 1568), (256, 2080)):
+        R, C = rans.pick_tiling(rows, cols)
+        assert C % 64 == 0 and rans.w64_stream_cols(cols) % C == 0
+        codes = _codes(rows, cols, seed=cols)
+        enc = rans.encode(codes, R, C, 1)
+        assert rans.tiling_of(enc) == (R, C, 1)
+        np.testing.assert_array_equal(rans.decode_ref(enc), codes)
+        np.testing.assert_array_equal(oracle.w64_decode(enc), codes)
+    with pytest.raises(AssertionError):
+        rans.encode(_codes(64, 128, 1), 16, 96)  # 96 divides neither 128 nor a padded width

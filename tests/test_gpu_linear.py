@@ -168,3 +168,49 @@ def test_linear_group_prefill_one_gemm(rans, lib):
         ref = x.double() @ wd.t() + m.bias.double()
         assert _rel(y, ref) <= 1e-2
         assert _rel(y.float(), own) <= 5e-3
+
+
+def test_linears_with_odd_multiple_of_32_inputs(rans, lib):
+    """in_features an odd multiple of 32 (96, 1568): RansLinear (GEMV and
+    prefill paths) and a grouped pair built by replace_linears match their
+    dense twins; the matrices are stored with 32 appended columns."""
+    import rans_linear as L
+    print("case RansLinear odd-32 in_features", flush=True)
+    g = torch.Generator().manual_seed(3)
+    for out_f, in_f in ((64, 96), (384, 1568)):
+        w = torch.randn(out_f, in_f, generator=g) * 0.02
+        codes, step = L.quantize_uniform(w, 4.0)
+        lin = L.RansLinear.from_codes(codes, step, None, lib, tune=False)
+        assert lin.matrix.stream_cols == in_f + 32
+        wd = torch.from_numpy(codes).double() * torch.from_numpy(step).double()
+        for shape in [(in_f,), (3, in_f), (20, in_f)]:
+            x = torch.randn(shape, generator=g)
+            y = lin(x.cuda())
+            ref = torch.nn.functional.linear(x.double(), wd)
+            assert _rel(y, ref) <= (1e-2 if len(shape) > 1 and shape[0] > 8 else 1e-3), shape
+
+    class Pair(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.gate_proj = torch.nn.Linear(96, 64, bias=False)
+            self.up_proj = torch.nn.Linear(96, 64, bias=False)
+
+        def forward(self, x):
+            return self.gate_proj(x) * self.up_proj(x)
+
+    torch.manual_seed(4)
+    model = Pair()
+    # the dense twin holds the same quantised weights (code * step)
+    wq = {}
+    for n in ("gate_proj", "up_proj"):
+        c, st = L.quantize_uniform(getattr(model, n).weight, 4.25)
+        wq[n] = torch.from_numpy(c).double() * torch.from_numpy(st).double()
+    names = L.replace_linears(model, bits=4.25, lib=lib, tune=False)
+    assert sorted(names) == ["gate_proj", "up_proj"]
+    assert model.gate_proj.group is not None and model.gate_proj.group is model.up_proj.group
+    model.cuda()
+    x = torch.randn(2, 96)
+    y = model(x.cuda())
+    xd = x.double()
+    ref = (xd @ wq["gate_proj"].T) * (xd @ wq["up_proj"].T)
+    assert _rel(y, ref) <= 2e-3

@@ -176,8 +176,8 @@ GROUPS = (("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj"))
 def replace_linears(module, bits=3.25, lib=None, skip=("lm_head",), tune=True, groups=GROUPS):
     """Swap every nn.Linear of `module` (except names containing an entry of
     `skip`) for a RansLinear quantised at `bits`.  Returns the names swapped.
-    Layers whose in_features is not a multiple of 64 (the w64 tile width)
-    are left dense.  Siblings named in one entry of `groups` (same parent,
+    Layers whose in_features is not a multiple of 32 (the reference's
+    column granularity) are left dense.  Siblings named in one entry of `groups` (same parent,
     same in_features) are encoded with one tiling and linked into a
     LinearGroup; groups=() links none."""
     lib = lib or rans.build()
@@ -189,7 +189,7 @@ def replace_linears(module, bits=3.25, lib=None, skip=("lm_head",), tune=True, g
             sub = children.get(cname)
             full = f"{name}.{cname}" if name else cname
             return (isinstance(sub, torch.nn.Linear) and not any(s in full for s in skip)
-                    and sub.in_features % 64 == 0)
+                    and sub.in_features % 32 == 0)
 
         tilings, links = {}, []
         for names_ in groups or ():
