@@ -195,3 +195,34 @@ def test_reference_format_exact_size_allocation(rans, lib, golden, dev):
     finally:
         torch.cuda.synchronize()
         hip.hipFree(ptr)
+
+
+def test_reference_format_unaligned_words(rans, lib, golden, dev):
+    """`words` starting 2 bytes into an allocation (not 16-byte aligned): the
+    spans are staged through registers instead of direct copies; same
+    decode and GEMV."""
+    rows, cols, R, C = (int(v) for v in golden["enc1_meta"])
+    print(f"case ref32 unaligned words {rows}x{cols}", flush=True)
+    w = golden["enc1_words"]
+    buf = torch.zeros(w.size + 1, dtype=torch.int16, device="cuda")
+    buf[1:] = torch.from_numpy(np.ascontiguousarray(w).view(np.int16)).cuda()
+    words = buf[1:]
+    assert words.data_ptr() % 16 != 0
+    offs = torch.from_numpy(golden["enc1_offs"].view(np.int32)).cuda()
+    table = torch.from_numpy(golden["enc1_table"].view(np.int32)).cuda()
+    codes = golden["enc1_codes"].astype(np.int64)
+    step = torch.full((cols,), 0.25, device="cuda")
+    out = torch.empty(rows, cols, device="cuda", dtype=torch.bfloat16)
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.launch_rans_decode(R, words.data_ptr(), offs.data_ptr(), table.data_ptr(),
+                                  step.data_ptr(), out.data_ptr(), rows, cols, C, st) == 0
+    want = (torch.from_numpy(codes.astype(np.float32)) * 0.25).bfloat16()
+    assert torch.equal(out.cpu().view(torch.int16), want.view(torch.int16))
+    x = torch.randn(cols, device="cuda")
+    y = torch.zeros(rows, device="cuda")
+    assert lib.launch_rans_gemv(R, words.data_ptr(), offs.data_ptr(), table.data_ptr(),
+                                x.data_ptr(), y.data_ptr(), rows, cols, C, st) == 0
+    import oracle as O
+    ref = O.gemv_f64(codes, x.cpu().numpy().astype(np.float64), np.ones(cols))
+    yv = y.cpu().numpy().astype(np.float64)
+    assert np.linalg.norm(yv - ref) / np.linalg.norm(ref) <= REL_L2

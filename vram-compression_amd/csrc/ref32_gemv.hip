@@ -53,8 +53,9 @@ struct Ref32Args {
     void* out;            // GEMV: y, f32 [rows]; decode: bf16 [rows][cols]
     int64_t words_avail;  // 16-bit words from `words` to the end of its allocation
     int rows, cols, C, ncb;
-    int nlanes;  // (rows/R) * (cols/C) * 32
-    int slot;    // LDS words per wave (a multiple of 8)
+    int nlanes;   // (rows/R) * (cols/C) * 32
+    int slot;     // LDS words per wave (a multiple of 8)
+    int words16;  // `words` is 16-byte aligned: stage with direct global->LDS copies
 };
 
 __device__ __forceinline__ uint32_t ref_lds_addr(const void* p) {
@@ -86,35 +87,40 @@ __device__ __forceinline__ uint16_t ref_bf16(float f) {
 }
 
 // One decode step (rans_gemv.cu:32-37) on the 8-byte image {freq | code<<24,
-// slot-cum}, with the next word read ahead.  Words in LDS: the select form
-// (the read-ahead word is long back when the select needs it).
-__device__ __forceinline__ int32_t ref_step_lds(uint32_t& st, uint32_t& ad, uint32_t& w,
+// slot-cum}, software-pipelined: e holds the table entry of this symbol,
+// read in the previous step, and the next entry is read as soon as the new
+// state exists, ahead of the word refill; the next word w is read ahead.
+// Words in LDS: the select form (the read-ahead word is long back when the
+// select needs it).
+__device__ __forceinline__ int32_t ref_step_lds(uint32_t& st, uint32_t& ad, uint32_t& w, uint2& e,
                                                 const uint2* tab) {
-    const uint2 e = tab[st & (kRefM - 1)];
-    const uint32_t ns = __umul24(e.x, st >> 12) + e.y;
+    const uint2 cur = e;
+    const uint32_t ns = __umul24(cur.x, st >> 12) + cur.y;
     const bool need = ns < kRefL;
     st = need ? ((ns << 16) | w) : ns;
+    e = tab[st & (kRefM - 1)];
     if (need) {
         ad += 2u;
         w = ref_lds_u16(ad);
     }
-    return (int32_t)e.x >> 24;
+    return (int32_t)cur.x >> 24;
 }
 
 // The same step with the words in global memory.  The renormalised state is
 // formed inside the branch (an asm statement the compiler cannot hoist), so
 // a wave waits for a lane's read-ahead word only when that lane consumes it.
-__device__ __forceinline__ int32_t ref_step_global(uint32_t& st, uint32_t& p, uint32_t& w,
+__device__ __forceinline__ int32_t ref_step_global(uint32_t& st, uint32_t& p, uint32_t& w, uint2& e,
                                                    const uint2* tab, __amdgpu_buffer_rsrc_t wrs) {
-    const uint2 e = tab[st & (kRefM - 1)];
-    const uint32_t ns = __umul24(e.x, st >> 12) + e.y;
+    const uint2 cur = e;
+    const uint32_t ns = __umul24(cur.x, st >> 12) + cur.y;
     st = ns;
     if (ns < kRefL) {
         asm volatile("v_lshl_or_b32 %0, %1, 16, %2" : "=v"(st) : "v"(ns), "v"(w));
         p += 1u;
         w = __builtin_amdgcn_raw_buffer_load_b16(wrs, (int)(p * 2u), 0, 0);
     }
-    return (int32_t)e.x >> 24;
+    e = tab[st & (kRefM - 1)];
+    return (int32_t)cur.x >> 24;
 }
 
 template <int R, bool DECODE>
@@ -164,15 +170,36 @@ __global__ void __launch_bounds__(64 * kRefMaxWaves) ref32_kernel(Ref32Args a) {
             const_cast<uint16_t*>(a.words) + w0, 0,
             (int)min((a.words_avail - w0) * 2, (int64_t)0x7FFFFFFF), kRefBufWord3);
         const int nfull = (int)min((w1 - w0 + 7) >> 3, (a.words_avail - w0) >> 3);
-        for (int j = lane; j < nfull; j += 64) {
-            auto v = __builtin_amdgcn_raw_buffer_load_b128(srs, j * 16, 0, 0);
-            *reinterpret_cast<decltype(v)*>(slot + 8 * j) = v;
+        if (a.words16) {
+            // 16-byte aligned words: direct global->LDS copies, all issued
+            // before the one wait (lane i's 16 bytes land at base + 16*i)
+            const uint4* src = reinterpret_cast<const uint4*>(a.words + w0);
+            for (int j0 = 0; j0 < nfull; j0 += 64)
+                if (j0 + lane < nfull)
+                    __builtin_amdgcn_global_load_lds(
+                        src + j0 + lane,
+                        (__attribute__((address_space(3))) void*)(slot + 8 * j0), 16, 0, 0);
+        } else {
+            // through registers, four chunks in flight per lane
+            using V4 = decltype(__builtin_amdgcn_raw_buffer_load_b128(srs, 0, 0, 0));
+            for (int j = lane; j < nfull; j += 256) {
+                V4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (j + 64 * u < nfull)
+                        v[u] = __builtin_amdgcn_raw_buffer_load_b128(srs, (j + 64 * u) * 16, 0, 0);
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (j + 64 * u < nfull)
+                        *reinterpret_cast<V4*>(slot + 8 * (j + 64 * u)) = v[u];
+            }
         }
         const int ntail = (int)(w1 - w0) - 8 * nfull;  // < 8
         if (lane < ntail)
             slot[8 * nfull + lane] =
                 __builtin_amdgcn_raw_buffer_load_b16(srs, (8 * nfull + lane) * 2, 0, 0);
     }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct copies have landed
     __syncthreads();
 
     // this lane's tile: rows rb*R.., columns cb*C + l + 32k
@@ -190,18 +217,22 @@ __global__ void __launch_bounds__(64 * kRefMaxWaves) ref32_kernel(Ref32Args a) {
                 outb[(int64_t)(rb * R + r) * a.cols + col0 + 32 * k] = ref_bf16((float)code * xv);
             else
                 acc[r] = fmaf((float)code, xv, acc[r]);
+            // consumed here: otherwise the compiler sinks the conversions
+            // and FMAs past the refill branches and reorders the reads
+            asm volatile("" : "+v"(acc[r]));
         };
         if (staged) {
             uint32_t ad = ref_lds_addr(slot + (p0 - (uint32_t)w0));
             uint32_t st = (ref_lds_u16(ad) << 16) | ref_lds_u16(ad + 2u);
             ad += 4u;
             uint32_t w = ref_lds_u16(ad);
+            uint2 e = tab[st & (kRefM - 1)];
             float xn = a.xs[col0];
             for (int k = 0; k < nk; k++) {
                 const float xv = xn;
                 xn = a.xs[col0 + 32 * min(k + 1, nk - 1)];
 #pragma unroll
-                for (int r = 0; r < R; r++) emit(k, r, ref_step_lds(st, ad, w, tab), xv);
+                for (int r = 0; r < R; r++) emit(k, r, ref_step_lds(st, ad, w, e, tab), xv);
             }
         } else {
             // ranged from the wave's first offset, so the byte offsets stay
@@ -217,10 +248,11 @@ __global__ void __launch_bounds__(64 * kRefMaxWaves) ref32_kernel(Ref32Args a) {
                           __builtin_amdgcn_raw_buffer_load_b16(wrs, (int)(p * 2u + 2u), 0, 0);
             p += 2u;
             uint32_t w = __builtin_amdgcn_raw_buffer_load_b16(wrs, (int)(p * 2u), 0, 0);
+            uint2 e = tab[st & (kRefM - 1)];
             for (int k = 0; k < nk; k++) {
                 const float xv = a.xs[col0 + 32 * k];
 #pragma unroll
-                for (int r = 0; r < R; r++) emit(k, r, ref_step_global(st, p, w, tab, wrs), xv);
+                for (int r = 0; r < R; r++) emit(k, r, ref_step_global(st, p, w, e, tab, wrs), xv);
             }
         }
     }
@@ -293,6 +325,7 @@ int ref32_entry(int R, const void* words, const void* offs, const void* table, c
     a.xs = static_cast<const float*>(xs);
     a.out = out;
     a.words_avail = avail;
+    a.words16 = ((uintptr_t)words & 15) == 0;
     a.rows = rows;
     a.cols = cols;
     a.C = C;
