@@ -224,8 +224,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--tiling", type=str, default=None, help="R,C,S")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--word-fetch", choices=("tune", "always", "refill"), default="tune",
-                    help="GEMV word-fetch policy; 'tune' times both on the matrix")
+    ap.add_argument("--word-fetch", choices=("tune", "always", "refill"), default="refill",
+                    help="GEMV word-fetch policy: refill (the library's default for tiles of "
+                         "3 or more rows), always, or tune (time both on the matrix; a 2x20-launch "
+                         "timing that can pick either within noise)")
     ap.add_argument("--no-rocblas", action="store_true")
     ap.add_argument("--no-chain", action="store_true",
                     help="skip the per-token chain (196 GEMVs, grouped launches)")
