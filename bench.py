@@ -242,7 +242,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the matrix would shard by tile rows; see DESIGN.md)", file=sys.stderr)
+              "(a matrix would shard by ranges of tile rows, one range per GPU)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
