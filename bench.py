@@ -241,7 +241,7 @@ def main():
                          "copies, then one 256 MiB device copy as the FETCH/WRITE calibration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
+        print("bench.py measures one GPU: the library has no multi-GPU path "
               "(a matrix would shard by ranges of tile rows, one range per GPU)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():

@@ -1,5 +1,5 @@
 """bench.py's command line without a GPU: more than one GPU is refused with
-a message (this build measures one), and so is a run on a host without a
+a message (the benchmark measures one), and so is a run on a host without a
 ROCm device; neither touches a GPU."""
 import os
 import subprocess
