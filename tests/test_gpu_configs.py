@@ -221,3 +221,33 @@ def test_ecsq_wf_fixture(rans, oracle, lib, dev):
     ref = oracle.gemv_f64(big, xb.float().cpu().numpy().astype(np.float64),
                           step.astype(np.float64))
     assert _rel_l2(m.gemv(xb).cpu().numpy(), ref) <= REL_L2
+
+
+def test_random_reference_tilings_on_gpu(rans, oracle, lib, dev):
+    """Seeded random shapes and (R, C) under the reference's preconditions
+    only (any R, C % 32 == 0, cols possibly an odd multiple of 32), mapped by
+    encode: decoded codes bit-exact, bf16 decode bit-exact, GEMV at a random
+    batch within the bar of the oracle; ~0.5% escapes."""
+    rng = np.random.default_rng(77)
+    for case in range(16):
+        R = int(rng.integers(1, 41))
+        C = 32 * int(rng.integers(1, 40))
+        rows = R * int(rng.integers(1, 5))
+        cols = C * int(rng.integers(1, 4))
+        batch = int(rng.integers(1, 6))
+        print(f"case random reference tiling {case}: {rows}x{cols} R={R} C={C} batch={batch}",
+              flush=True)
+        codes = oracle.synth_codes(rows, cols, float(rng.uniform(1.5, 5.5)), seed=100 + case)
+        codes[0, 0], codes[-1, -1] = 5, -5
+        hit = rng.random(codes.shape) < 0.005
+        codes[hit] = rng.integers(128, 3000, size=int(hit.sum())) * rng.choice([-1, 1], int(hit.sum()))
+        step = (rng.random(cols) + 0.25).astype(np.float32)
+        m = rans.RansMatrix(rans.encode(codes, R, C), torch.from_numpy(step), lib)
+        np.testing.assert_array_equal(m.decode_codes().cpu().numpy(), codes)
+        want = (torch.from_numpy(codes.astype(np.float32)) * torch.from_numpy(step)).bfloat16()
+        assert torch.equal(m.decode().cpu().view(torch.int16), want.view(torch.int16))
+        x = torch.from_numpy(rng.standard_normal((batch, cols)).astype(np.float32)).cuda().bfloat16()
+        y = m.gemv(x).cpu().numpy()
+        ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64), step.astype(np.float64))
+        for b in range(batch):
+            assert _rel_l2(y[b], ref[b]) <= REL_L2, (case, b)
