@@ -65,8 +65,8 @@ extern "C" {
 /* rejected-argument return values */
 #define RANS_EUNSUPPORTED (-1) /* R, S or batch without a compiled kernel: the GPU entry
                                   points take R in {1, 2, 3, 4, 8, 16} with S in {1, 2, 4},
-                                  and R = 35 with S = 1 (the encoder and host decoder take
-                                  any R <= 256) */
+                                  and R in {20, 35} with S = 1 (the encoder and host
+                                  decoder take any R <= 256) */
 #define RANS_EGEOMETRY (-2)    /* shape not divisible, or tile too large for LDS */
 #define RANS_EWORKSPACE (-3)   /* split-K workspace missing or too small */
 #define RANS_EARG (-4)         /* null pointer or negative size */

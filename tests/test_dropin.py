@@ -270,3 +270,39 @@ def test_pick_tiling_odd_multiple_of_32(rans, oracle):
         np.testing.assert_array_equal(oracle.w64_decode(enc), codes)
     with pytest.raises(AssertionError):
         rans.encode(_codes(64, 128, 1), 16, 96)  # 96 divides neither 128 nor a padded width
+
+
+def test_pick_tiling_large_matrix_rounds(rans):
+    """Above 32M weights pick_tiling weighs the launch's last round of
+    resident workgroups: 25600x5120 takes 20x640 tiles (1280 tile rows, the
+    last of 768-workgroup rounds two thirds full) over 16x640 (1600 tile
+    rows, the last round 8% full), 5120x17408 keeps 4x2176 over 8x2176 (last
+    round a quarter full), and the other benchmark shapes keep their
+    tilings.  Below 32M weights the 20-row height is not a candidate."""
+    assert rans.pick_tiling(25600, 5120) == (20, 640)
+    assert rans.pick_tiling(25600, 5120, bits=2.25) == (20, 640)
+    assert rans.pick_tiling(5120, 17408) == (4, 2176)
+    assert rans.pick_tiling(5120, 25600) == (4, 3200)
+    assert rans.pick_tiling(34816, 5120) == (16, 640)
+    assert rans.pick_tiling(1536, 8960) == (3, 2240)
+    assert rans.pick_tiling(8960, 1536) == (35, 192)
+    assert rans.pick_tiling(2560, 5120)[0] != 20  # 13M weights
+    rounds, fill = rans.last_round_fill(25600, 5120, 16, 640, bits=2.25)
+    assert rounds > 2 and fill < 0.1
+    rounds, fill = rans.last_round_fill(25600, 5120, 20, 640, bits=2.25)
+    assert 1 < rounds < 2 and fill > 0.6
+    assert rans.last_round_fill(5120, 17408, 8, 2176)[1] < 0.5
+    # two states per lane never take the 20-row (one state per lane) height
+    assert rans.pick_tiling(25600, 5120, S=2)[0] != 20
+    assert rans.w64_tiling(40, 1280, 20, 640, 2)[0] != 20
+
+
+def test_r20_round_trip(rans, oracle):
+    """The 20-row height through the host encoder and both host decoders,
+    escapes included; encode keeps (20, C, 1) as given."""
+    codes = _codes(60, 1280, seed=20)
+    codes[5, 7], codes[59, 1279] = 300, -1000
+    enc = rans.encode(codes, 20, 640, 1)
+    assert rans.tiling_of(enc) == (20, 640, 1)
+    np.testing.assert_array_equal(rans.decode_ref(enc), codes)
+    np.testing.assert_array_equal(oracle.w64_decode(enc), codes)

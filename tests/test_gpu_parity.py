@@ -433,13 +433,52 @@ def test_r35_tiles(rans, oracle, lib, dev, rows, cols, C, batch):
             m2.gemv(x)
 
 
+@pytest.mark.parametrize("rows,cols,C,batch", [
+    (20, 192, 192, 4),         # one tile, one wave: 80 (row, batch) sums
+    (40, 1280, 640, 4),        # two tile rows of two column tiles
+    (60, 1024, 64, 3),         # 16 column tiles: two column groups (split reduction)
+    (2560, 5120, 640, 1),      # 128 tile rows of the 25600x5120 tiling
+])
+def test_r20_tiles(rans, oracle, lib, dev, rows, cols, C, batch):
+    """Tiles of 20 rows (one state per lane, the large-matrix height):
+    codes bit-exact, bf16 decode bit-exact, GEMV against the float64 oracle
+    with ~0.2% escapes for both word-fetch policies (bitwise equal) at batch
+    1, 3 and 4, and with both table-entry layouts forced (bitwise equal)."""
+    print(f"case r20 {rows}x{cols} C={C} batch={batch}", flush=True)
+    rng = np.random.default_rng(rows + cols)
+    codes = oracle.synth_codes(rows, cols, 2.5, seed=rows)
+    codes[0, 0], codes[-1, -1] = 5, -5
+    hit = rng.random(codes.shape) < 0.002
+    codes[hit] = rng.integers(128, 900, size=int(hit.sum())) * rng.choice([-1, 1], int(hit.sum()))
+    step = (rng.random(cols) + 0.25).astype(np.float32)
+    enc = rans.encode(codes, 20, C, 1)
+    assert rans.tiling_of(enc) == (20, C, 1)
+    x = torch.from_numpy(rng.standard_normal((batch, cols)).astype(np.float32)).cuda().bfloat16()
+    ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64), step.astype(np.float64))
+    ys = []
+    for flags in (rans.F_WORDS_ALWAYS, rans.F_WORDS_REFILL, rans.F_WORDS_REFILL | rans.F_TABLE4,
+                  rans.F_WORDS_REFILL | rans.F_TABLE8):
+        m = rans.RansMatrix(enc, torch.from_numpy(step), lib, flags=flags)
+        np.testing.assert_array_equal(m.decode_codes().cpu().numpy(), codes)
+        y = m.gemv(x).cpu()
+        for b in range(batch):
+            assert _rel_l2(y[b].numpy(), ref[b]) <= REL_L2, (flags, b)
+        ys.append(y)
+        y1 = m.gemv(x[0]).cpu()
+        assert _rel_l2(y1.numpy(), ref[0]) <= REL_L2, flags
+    assert all(torch.equal(ys[0], y) for y in ys[1:])
+    dec = m.decode().cpu()
+    want = (torch.from_numpy(codes.astype(np.float32)) * torch.from_numpy(step)).bfloat16()
+    assert torch.equal(dec.view(torch.int16), want.view(torch.int16))
+
+
 @pytest.mark.parametrize("R,C", [(1, 256), (2, 256), (3, 512), (4, 256), (8, 512), (16, 128),
-                                 (35, 192)])
+                                 (20, 512), (35, 192)])
 def test_table_entry_layouts_agree(rans, oracle, lib, dev, R, C):
     """The 8-byte and the 4-byte LDS table entries decode the same symbols:
     forced either way, GEMV outputs are bitwise equal at batch 1, 4 and 5
     (f32 and bf16 x), escapes included, and match the oracle."""
-    rows, cols = 35 * 24 if R == 35 else 384, 1536
+    rows, cols = {35: 35 * 24, 20: 20 * 24}.get(R, 384), 1536
     print(f"case table entries R={R} C={C}", flush=True)
     codes = oracle.synth_codes(rows, cols, 3.25, seed=R * 7 + 1)
     codes[3, 11] = 250  # escapes of both signs
@@ -541,7 +580,7 @@ def test_table_choice_inside_graph_capture(rans, oracle, lib, dev):
     assert torch.equal(m.gemv(x), y8)
 
 
-@pytest.mark.parametrize("R,C", [(3, 256), (16, 128), (35, 192)])
+@pytest.mark.parametrize("R,C", [(3, 256), (16, 128), (20, 640), (35, 192)])
 def test_escape_value_extremes(rans, oracle, lib, dev, R, C):
     """The side table's 16-bit values at their extremes (-32768, 32767, and
     the smallest escapes -128 and 128) come back through the kernels'

@@ -420,14 +420,15 @@ __device__ __forceinline__ void lds_add(float* p, float v) {
     __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Escapes of tall tiles (R >= 32) go to the reduced row sums in LDS with one
-// float add per lane and batch row instead of 2R + RB VALU instructions per
-// chunk.  That pays while the LDS is otherwise idle: R = 35 tiles run two
-// waves per SIMD.  With four waves per SIMD (large matrices, 16-row tiles)
-// the atomics, serialised on the CU's one LDS, cost more than the FMAs
-// (25600x5120 with 1% escapes: +6% at batch 1, +38% at batch 4).
+// Escapes of 35-row tiles go to the reduced row sums in LDS with one float
+// add per lane and batch row instead of 2R + RB VALU instructions per chunk.
+// That pays while the LDS is otherwise idle: R = 35 tiles run two waves per
+// SIMD (8960 x 1536).  With four waves per SIMD (large matrices, 16-row
+// tiles) the atomics, serialised on the CU's one LDS, cost more than the
+// FMAs (25600x5120 with 1% escapes: +6% at batch 1, +38% at batch 4), so
+// 20-row tiles (made for large matrices) keep the FMAs.
 template <int R>
-constexpr bool kEscapesInLds = R >= 32;
+constexpr bool kEscapesInLds = R == 35;
 
 // GROUP: a grouped launch (several matrices, slot found per workgroup);
 // otherwise slot 0 only, read at fixed kernel-argument offsets.  T4: the
@@ -435,8 +436,18 @@ constexpr bool kEscapesInLds = R >= 32;
 // ROWS2: each workgroup takes two adjacent tile rows, W/2 waves each, so
 // one table copy serves twice the waves (single pass over the columns
 // only: no split-K).
+// Waves per SIMD the register allocation must allow: 4 for the batch-4
+// kernel on 20-row tiles, whose 80 accumulators otherwise take it to 130
+// VGPRs and 3 waves per SIMD (25600x5120 at batch 4: 86.5 us; at 128
+// VGPRs, one register spilled outside the decode loop, 61.8 us); 1 (no
+// constraint) elsewhere.
+template <int R, int B>
+constexpr int kMinWavesPerEu = (R == 20 && B == 4) ? 4 : 1;
+
 template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP, bool T4, bool ROWS2>
-__global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_gemv_kernel(GemvArgs a) {
+__global__ void __launch_bounds__(64 * kMaxWaves)
+    __attribute__((amdgpu_waves_per_eu(kMinWavesPerEu<R, B>)))
+    rans_w64_gemv_kernel(GemvArgs a) {
     __shared__ __align__(16) TabEntry<T4> tab[kProbM];
     __shared__ float red[kMaxWaves * R * B];
     __shared__ int flag[4];
@@ -1051,7 +1062,8 @@ GemvFn gemv_fn_t() {
 // var: bit 0 = bf16 x, bit 1 = refill-only word fetch, bit 2 = grouped
 // launch, bit 3 = 4-byte table entries, bit 4 = two tile rows per
 // workgroup (bits 2-4 compiled for one state per lane only, at most one of
-// them, and bit 4 not for 35-row tiles).
+// them; tiles taller than 16 rows have no paired-row kernels, and of them
+// only the 35-row ones have grouped kernels).
 template <int R, int S, int B, bool GROUP, bool T4, bool ROWS2>
 GemvFn gemv_fn_xf(int var) {
     switch (var & 3) {
@@ -1066,9 +1078,10 @@ template <int R, int S, int B>
 GemvFn gemv_fn_v(int var) {
     if (var & 28) {
         if constexpr (S == 1) {
-            if ((var & 28) == 4) return gemv_fn_xf<R, S, B, true, false, false>(var);
+            if constexpr (R <= 16 || R == 35)
+                if ((var & 28) == 4) return gemv_fn_xf<R, S, B, true, false, false>(var);
             if ((var & 28) == 8) return gemv_fn_xf<R, S, B, false, true, false>(var);
-            if constexpr (R != 35)
+            if constexpr (R <= 16)
                 if ((var & 28) == 16) return gemv_fn_xf<R, S, B, false, false, true>(var);
         }
         return {nullptr, 0};
@@ -1103,6 +1116,7 @@ GemvFn gemv_fn(int R, int S, int B, int var) {
         case 4: return gemv_fn_s<4>(S, B, var);
         case 8: return gemv_fn_s<8>(S, B, var);
         case 16: return gemv_fn_s<16>(S, B, var);
+        case 20: return S == 1 ? gemv_fn_b<20, 1>(B, var) : GemvFn{nullptr, 0};
         case 35: return S == 1 ? gemv_fn_b<35, 1>(B, var) : GemvFn{nullptr, 0};
         default: return {nullptr, 0};
     }
@@ -1181,13 +1195,13 @@ int device_cus() {
 // every CU a workgroup: 1536x1536 in 8x384 tiles (192 workgroups) ran 3-5%
 // slower as 96.  Single-matrix launches with one state per lane, one
 // workgroup per tile row (no split-K), at most 4 waves per row, an even
-// number of tile rows and the 8-byte table entries; not 35-row tiles.  The
-// paired workgroup holds both rows' staged blocks, so it is only taken when
-// twice the dynamic LDS (lds bytes for one row's waves) still fits beside
-// the static arrays.
+// number of tile rows and the 8-byte table entries; not tiles taller than
+// 16 rows.  The paired workgroup holds both rows' staged blocks, so it is
+// only taken when twice the dynamic LDS (lds bytes for one row's waves)
+// still fits beside the static arrays.
 bool use_rows2(const rans_w64_matrix* m, int n, int v, int waves, int ngroups, int grid,
                size_t lds) {
-    if (n != 1 || m->S != 1 || (v & 8) || m->R == 35 || ngroups != 1) return false;
+    if (n != 1 || m->S != 1 || (v & 8) || m->R > 16 || ngroups != 1) return false;
     if (2 * waves > kMaxWaves || (m->rows / m->R) % 2) return false;
     if (2 * lds + gemv_static_lds(m->R) > (size_t)kLdsMax) return false;
     const int cus = device_cus();
@@ -1209,12 +1223,17 @@ bool use_table4(const rans_w64_matrix* m, int B, int var, int waves, size_t lds,
     return resident > 0 && grid > resident;
 }
 
-// R = 35 (one state per lane only) splits rows of 8960 = 256 x 35 into 256
-// tile rows, so that 8960 x 1536 (Qwen2.5-1.5B's gate and up projections)
-// runs as 2048 tiles of 35 x 192: two waves on every SIMD.
+// Tiles taller than 16 rows take one state per lane.  R = 35 splits rows of
+// 8960 = 256 x 35 into 256 tile rows, so that 8960 x 1536 (Qwen2.5-1.5B's
+// gate and up projections) runs as 2048 tiles of 35 x 192: two waves on
+// every SIMD.  R = 20 is for large matrices, whose launches take more than
+// one round of resident workgroups: 25600 rows make 1280 tile rows instead
+// of 1600 with R = 16, so the last of the rounds of 768 workgroups is two
+// thirds full instead of 8% (25600x5120 at batch 1: 54.8 -> 51.9 us), with
+// fewer, longer states (2.923 -> 2.880 bits/weight).
 bool supported_rs(int R, int S) {
     return ((R == 1 || R == 2 || R == 3 || R == 4 || R == 8 || R == 16) && (S == 1 || S == 2 || S == 4)) ||
-           (R == 35 && S == 1);
+           ((R == 20 || R == 35) && S == 1);
 }
 
 template <int R, int S, int MODE>
@@ -1234,7 +1253,7 @@ int dispatch_decode(const DecodeArgs& a, int R, int S, int waves, size_t lds, in
     if (R == RR && S == SS) return launch_decode_t<RR, SS, MODE>(a, waves, lds, grid, st);
 #define VRAMC_DEC_R(RR) VRAMC_DEC_CASE(RR, 1) VRAMC_DEC_CASE(RR, 2) VRAMC_DEC_CASE(RR, 4)
     VRAMC_DEC_R(1) VRAMC_DEC_R(2) VRAMC_DEC_R(3) VRAMC_DEC_R(4) VRAMC_DEC_R(8) VRAMC_DEC_R(16)
-    VRAMC_DEC_CASE(35, 1)
+    VRAMC_DEC_CASE(20, 1) VRAMC_DEC_CASE(35, 1)
 #undef VRAMC_DEC_R
 #undef VRAMC_DEC_CASE
     return RANS_EUNSUPPORTED;
