@@ -365,7 +365,7 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
     else:
         step = torch.from_numpy(np.asarray(step, np.float32))
     if R is None or C is None:
-        R, C = pick_tiling(rows, cols, S=S)
+        R, C = pick_tiling(rows, cols, S=S, bits=bits)
     enc = encode(codes, R, C, S)
     m = rans.RansMatrix(enc, step, lib)
     flags = m.tune(batch=batch)
@@ -568,13 +568,16 @@ def configs():
               flush=True)
 
 
-def profile(rows=25600, cols=5120, bits=2.25, dist="student3", escape_frac=0.01, R=16, C=640,
+def profile(rows=25600, cols=5120, bits=2.25, dist="student3", escape_frac=0.01, R=0, C=0,
             launches=20, fetch="refill"):
     """One encoded matrix launched `launches` times at batch 1, then at
     batch 4 (bf16 x), for a profiler run: rans_bench.py profile [ROWS COLS
     BITS DIST ESC R C LAUNCHES FETCH].  The defaults are the 27B-class
-    25600x5120 matrix of the configurations."""
+    25600x5120 matrix of the configurations; R = C = 0 takes the library's
+    tiling (pick_tiling at these bits)."""
     lib = rans.build()
+    if not R or not C:
+        R, C = pick_tiling(rows, cols, bits=bits)
     codes = synth_codes_full(rows, cols, bits, dist=dist, seed=rows + cols, escape_frac=escape_frac)
     step = torch.from_numpy(lognormal_steps(cols, seed=rows + cols))
     flags = {"always": rans.F_WORDS_ALWAYS, "refill": rans.F_WORDS_REFILL}[fetch]
