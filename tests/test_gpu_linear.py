@@ -24,9 +24,10 @@ def test_ranslinear_matches_dense(rans, lib):
     codes, step = L.quantize_uniform(w, 4.0)
     codes[7, 9] = 400  # an escape
     lin = L.RansLinear.from_codes(codes, step, b, lib)
+    assert lin.matrix.fused_rows_limit == 16  # 8-row tiles: the batch-8 kernel
     wd = torch.from_numpy(codes).double() * torch.from_numpy(step).double()
     tol = {torch.float32: 1e-3, torch.bfloat16: 8e-3, torch.float16: 2e-3}
-    for shape in [(1536,), (3, 1536), (2, 4, 1536)]:  # fused GEMV path: up to 8 rows
+    for shape in [(1536,), (3, 1536), (2, 4, 1536), (12, 1536)]:  # fused GEMV path
         for dt in (torch.float32, torch.bfloat16, torch.float16):
             x = torch.randn(shape, generator=g).to(dt)
             y = lin(x.cuda())
@@ -69,8 +70,9 @@ def test_tiny_qwen2_with_rans_linears(rans, lib):
         a = dense(ids).logits
         b = coded(ids).logits
         assert _rel(b, a) <= 1e-3
-        # a longer prompt takes the prefill path (bf16-decoded weights + dense GEMM)
-        long_ids = torch.randint(0, 512, (1, 12), generator=torch.Generator().manual_seed(2)).cuda()
+        # a longer prompt (more rows than any matrix's fused_rows_limit) takes
+        # the prefill path (bf16-decoded weights + dense GEMM)
+        long_ids = torch.randint(0, 512, (1, 20), generator=torch.Generator().manual_seed(2)).cuda()
         assert _rel(coded(long_ids).logits, dense(long_ids).logits) <= 2e-2
         # one decode step: two grouped launches per layer (q/k/v, gate/up)
         calls = []

@@ -553,7 +553,9 @@ def test_table_choice_inside_graph_capture(rans, oracle, lib, dev):
     assert m.table_lds4 is not None
     assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, 1) == 1
     assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, 4) == 0
-    assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, 5) == 1
+    # 5 vectors are one batch-8 launch (8-byte entries); 9 add a batch-1 one
+    assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, 5) == 0
+    assert lib.rans_gemv_table4(ctypes.byref(m._desc), rans.X_BF16, 9) == 1
     x = torch.randn(cols, device="cuda")
     base = m._desc.flags & ~(rans.F_TABLE4 | rans.F_TABLE8)
     # load both kernels outside the capture; forced choices skip the query
@@ -633,3 +635,28 @@ def test_two_tile_rows_odd_and_even(rans, oracle, lib, dev, tile_rows):
         ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64),
                               step.numpy().astype(np.float64))
         assert _rel_l2(y.numpy(), ref) <= REL_L2
+
+
+@pytest.mark.parametrize("R,C", [(1, 256), (3, 2240), (8, 384), (16, 256)])
+def test_batch_kernels_agree(rans, oracle, lib, dev, R, C):
+    """The batch-1, -4 and -8 kernels sum each vector's products in the same
+    order: a batch of 1 to 9 vectors, however it is split into launches
+    (5 to 8 vectors on the batch-8 kernel where tiles have at most 8 rows,
+    chunks of 4 on the batch-4 kernel otherwise, a single vector on the
+    batch-1 kernel), gives bitwise the outputs of one launch per vector, with
+    escapes, and matches the float64 oracle."""
+    rows, cols = {1: 64, 3: 384, 8: 256, 16: 256}[R], {256: 1024, 2240: 4480, 384: 1536}[C]
+    print(f"case batch kernels R={R} C={C}", flush=True)
+    codes = oracle.synth_codes(rows, cols, 3.25, seed=R)
+    rng = np.random.default_rng(R)
+    hit = rng.random(codes.shape) < 0.003
+    codes[hit] = rng.integers(128, 700, size=int(hit.sum())) * rng.choice([-1, 1], int(hit.sum()))
+    step = np.exp(0.4 * rng.standard_normal(cols)).astype(np.float32)
+    m = rans.RansMatrix(rans.encode(codes, R, C, 1), torch.from_numpy(step), lib)
+    x = torch.from_numpy(rng.standard_normal((9, cols)).astype(np.float32)).cuda().bfloat16()
+    singles = torch.stack([m.gemv(x[b]) for b in range(9)]).cpu()
+    ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64), step.astype(np.float64))
+    for batch in range(1, 10):
+        y = m.gemv(x[:batch]).cpu()
+        assert torch.equal(y, singles[:batch]), batch
+    assert _rel_l2(singles.numpy(), ref) <= REL_L2

@@ -52,13 +52,17 @@ constexpr int kMaxWaves = 8;
 template <bool T4>
 using TabEntry = std::conditional_t<T4, uint32_t, uint2>;
 
+// Largest batch a GEMV kernel is compiled for with tiles of R rows: 8 for
+// tiles of at most 8 rows (one state per lane only), 4 otherwise.
+constexpr int gemv_max_batch(int R) { return R <= 8 ? 8 : 4; }
+
 // LDS: the expanded table and the reduction scratch are static __shared__
 // arrays (their offsets are compile-time constants, so table addressing
 // needs no base add); the per-wave regions are dynamic.  The GEMV's
-// reduction scratch holds R*B floats per wave: the host reserves it for a
-// batch of 4 (the largest compiled), plus the 16-byte arrival flag.
+// reduction scratch holds R*B floats per wave: the host reserves it for the
+// largest batch compiled for R, plus the 16-byte arrival flag.
 constexpr int gemv_static_lds(int R, bool t4 = false) {
-    return (t4 ? 4 : 8) * (int)kProbM + 4 * kMaxWaves * R * 4 + 16;
+    return (t4 ? 4 : 8) * (int)kProbM + 4 * kMaxWaves * R * gemv_max_batch(R) + 16;
 }
 constexpr int kDecodeStaticLds = (int)sizeof(TabEntry<false>) * (int)kProbM;
 constexpr int kLdsMax = 160 * 1024;
@@ -436,13 +440,14 @@ constexpr bool kEscapesInLds = R == 35;
 // ROWS2: each workgroup takes two adjacent tile rows, W/2 waves each, so
 // one table copy serves twice the waves (single pass over the columns
 // only: no split-K).
-// Waves per SIMD the register allocation must allow: 4 for the batch-4
-// kernel on 20-row tiles, whose 80 accumulators otherwise take it to 130
-// VGPRs and 3 waves per SIMD (25600x5120 at batch 4: 86.5 us; at 128
-// VGPRs, one register spilled outside the decode loop, 61.8 us); 1 (no
+// Waves per SIMD the register allocation must allow: 4 for the kernels
+// with 64 or more accumulators beside the decode state (the batch-4 kernel
+// on 20-row tiles and the batch-8 kernel on 8-row tiles), which otherwise
+// take 130 VGPRs and 3 waves per SIMD (25600x5120 at batch 4: 86.5 us; at
+// 128 VGPRs, one register spilled outside the decode loop, 61.8 us); 1 (no
 // constraint) elsewhere.
 template <int R, int B>
-constexpr int kMinWavesPerEu = (R == 20 && B == 4) ? 4 : 1;
+constexpr int kMinWavesPerEu = ((R == 20 && B == 4) || (R == 8 && B == 8)) ? 4 : 1;
 
 template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP, bool T4, bool ROWS2>
 __global__ void __launch_bounds__(64 * kMaxWaves)
@@ -683,23 +688,19 @@ __global__ void __launch_bounds__(64 * kMaxWaves)
         }
     }
 
+    // Every (row, batch) sum goes through the transpose-reduce, whatever
+    // R*B: its lanes pair in the same order for any value count, so the
+    // batch-1, -4 and -8 kernels give bitwise the same sum for a vector, and
+    // a batch split into chunks differently (grouped, paired rows, either
+    // table layout) gives the same results.
     constexpr int NRB = R * B;
-    if constexpr (NRB >= 8) {
+    {
         float w[NRB];
 #pragma unroll
         for (int r = 0; r < R; r++)
 #pragma unroll
             for (int b = 0; b < B; b++) w[r * B + b] = acc[r][b];
         transpose_sum_store<0, NRB, NRB>(w, red + wave * NRB, lane);
-    } else {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-#pragma unroll
-            for (int b = 0; b < B; b++) {
-                const float v = wave_sum63(acc[r][b]);
-                if (lane == 63) red[wave * NRB + r * B + b] = v;
-            }
-        }
     }
 
     // Tall tiles: the escapes added to the wave's reduced sums, each lane
@@ -1063,7 +1064,8 @@ GemvFn gemv_fn_t() {
 // launch, bit 3 = 4-byte table entries, bit 4 = two tile rows per
 // workgroup (bits 2-4 compiled for one state per lane only, at most one of
 // them; tiles taller than 16 rows have no paired-row kernels, and of them
-// only the 35-row ones have grouped kernels).
+// only the 35-row ones have grouped kernels; the batch-8 kernels have only
+// the plain and paired-row variants).
 template <int R, int S, int B, bool GROUP, bool T4, bool ROWS2>
 GemvFn gemv_fn_xf(int var) {
     switch (var & 3) {
@@ -1078,9 +1080,10 @@ template <int R, int S, int B>
 GemvFn gemv_fn_v(int var) {
     if (var & 28) {
         if constexpr (S == 1) {
-            if constexpr (R <= 16 || R == 35)
+            if constexpr ((R <= 16 || R == 35) && B != 8)
                 if ((var & 28) == 4) return gemv_fn_xf<R, S, B, true, false, false>(var);
-            if ((var & 28) == 8) return gemv_fn_xf<R, S, B, false, true, false>(var);
+            if constexpr (B != 8)
+                if ((var & 28) == 8) return gemv_fn_xf<R, S, B, false, true, false>(var);
             if constexpr (R <= 16)
                 if ((var & 28) == 16) return gemv_fn_xf<R, S, B, false, false, true>(var);
         }
@@ -1094,6 +1097,9 @@ GemvFn gemv_fn_b(int B, int var) {
     switch (B) {
         case 1: return gemv_fn_v<R, S, 1>(var);
         case 4: return gemv_fn_v<R, S, 4>(var);
+        case 8:
+            if constexpr (S == 1 && gemv_max_batch(R) == 8) return gemv_fn_v<R, S, 8>(var);
+            return {nullptr, 0};
         default: return {nullptr, 0};
     }
 }
@@ -1319,6 +1325,51 @@ SplitK workspace_splitk(const rans_w64_matrix* m, int batch) {
             reinterpret_cast<float*>(static_cast<uint8_t*>(m->workspace) + counters_bytes(m))};
 }
 
+// One launch of a batch's chunk: nb vectors from vector `first` on the
+// batch-B kernel, variant bits v (bit 3: 4-byte table entries, bit 4: two
+// tile rows per workgroup).
+struct GemvChunk {
+    int first, nb, B, v;
+};
+
+// The launches a GEMV of `batch` vectors makes, in order, each passed to
+// fn (which returns 0 to go on; its first nonzero value is returned).
+// Five to eight remaining vectors run as one launch of the batch-8 kernel
+// where one is compiled for the tiling and the chunk's variant (one state
+// per lane, tiles of at most 8 rows, a single pass over the columns: no
+// split-K); otherwise up to 4 run on the batch-4 kernel, and a single
+// remaining vector on the batch-1 kernel.  The batch kernels take an
+// active-vector count, so a remainder is one launch.  Table entries and
+// row pairing are chosen per chunk; t4_image: whether a 4-byte table image
+// is (or would be) there to choose.
+template <class F>
+int plan_gemv(const rans_w64_matrix* m0, int n, int var, int waves, int ngroups, size_t lds,
+              int grid, int batch, bool t4_image, F fn) {
+    auto variant = [&](int B) {
+        int v = var;
+        if (n == 1 && t4_image && use_table4(m0, B, var, waves, lds, grid)) v |= 8;
+        if (use_rows2(m0, n, v, waves, ngroups, grid, lds)) v |= 16;
+        return v;
+    };
+    int done = 0;
+    while (done < batch) {
+        const int left = batch - done;
+        GemvChunk c{done, 0, 0, 0};
+        if (left >= 5 && ngroups == 1) {
+            const int v = variant(8);
+            if (gemv_fn(m0->R, m0->S, 8, v).fn) c = {done, left >= 8 ? 8 : left, 8, v};
+        }
+        if (!c.nb) {
+            const int B = left >= 2 ? 4 : 1;
+            c = {done, left >= 4 ? 4 : (left >= 2 ? left : 1), B, variant(B)};
+        }
+        const int rc = fn(c);
+        if (rc != 0) return rc;
+        done += c.nb;
+    }
+    return 0;
+}
+
 // One launch over n matrices that share x (n = 1: any single matrix,
 // split-K included, with its buffers in sk; n > 1: a group, validated by
 // the caller, never split).
@@ -1368,31 +1419,20 @@ int launch_gemv_common(const rans_w64_matrix* const* ms, int n, const void* x, i
     }
     const size_t lds = (size_t)waves * a.wave_words * 2;
 
-    // Batches run in chunks of up to 4 vectors on the batch-4 kernel, a
-    // single remaining vector on the batch-1 kernel.
-    int done = 0;
-    while (done < batch) {
-        const int nb = batch - done >= 4 ? 4 : batch - done;
-        const int B = nb >= 2 ? 4 : 1;
-        a.x = static_cast<const uint8_t*>(x) + (size_t)done * m0->cols * xsz;
-        for (int i = 0; i < n; i++) a.mat[i].y = ys[i] + (size_t)done * ms[i]->rows;
-        a.nb = nb;
-        int v = var;
-        if (n == 1 && (m0->flags & RANS_F_TABLE4 || m0->table_lds4) &&
-            use_table4(m0, B, var, waves, lds, grid))
-            v |= 8;
+    const bool t4_image = (m0->flags & RANS_F_TABLE4) || m0->table_lds4;
+    return plan_gemv(m0, n, var, waves, ngroups, lds, grid, batch, t4_image,
+                     [&](const GemvChunk& c) {
+        a.x = static_cast<const uint8_t*>(x) + (size_t)c.first * m0->cols * xsz;
+        for (int i = 0; i < n; i++) a.mat[i].y = ys[i] + (size_t)c.first * ms[i]->rows;
+        a.nb = c.nb;
         if (n == 1)
             a.mat[0].table_lds =
-                reinterpret_cast<const uint4*>((v & 8) ? m0->table_lds4 : m0->table_lds);
-        const bool rows2 = use_rows2(m0, n, v, waves, ngroups, grid, lds);
-        if (rows2) v |= 16;
+                reinterpret_cast<const uint4*>((c.v & 8) ? m0->table_lds4 : m0->table_lds);
+        const bool rows2 = (c.v & 16) != 0;
         a.W = rows2 ? 2 * waves : waves;
-        const int rc = launch_gemv_fn(gemv_fn(m0->R, m0->S, B, v), a, a.W, rows2 ? 2 * lds : lds,
-                                      rows2 ? grid / 2 : grid, stream);
-        if (rc != 0) return rc;
-        done += nb;
-    }
-    return 0;
+        return launch_gemv_fn(gemv_fn(m0->R, m0->S, c.B, c.v), a, a.W, rows2 ? 2 * lds : lds,
+                              rows2 ? grid / 2 : grid, stream);
+    });
 }
 
 bool check_gemv_args(const rans_w64_matrix* m, const void* x, int x_dtype, int batch,
@@ -1454,12 +1494,11 @@ extern "C" int rans_gemv_table4(const rans_w64_matrix* m, int x_dtype, int batch
     const bool refill = fetch == RANS_F_WORDS_REFILL || (fetch == 0 && m->R >= 3);
     const int var = (x_dtype == RANS_X_BF16 ? 1 : 0) | (refill ? 2 : 0);
     const size_t lds = (size_t)waves * wave_layout(m).raw_words * 2;
-    const int grid = (m->rows / m->R) * ((m->cols / m->C) / waves);
-    // the batch-4 kernel runs chunks of 2 to 4 vectors, the batch-1 kernel a
-    // single remaining one (as launch_gemv_common splits a batch)
-    if (batch >= 2 && use_table4(m, 4, var, waves, lds, grid)) return 1;
-    if (batch % 4 == 1 && use_table4(m, 1, var, waves, lds, grid)) return 1;
-    return 0;
+    const int ngroups = (m->cols / m->C) / waves;
+    const int grid = (m->rows / m->R) * ngroups;
+    // the launches rans_w64_gemv makes, were the 4-byte image there
+    return plan_gemv(m, 1, var, waves, ngroups, lds, grid, batch, true,
+                     [](const GemvChunk& c) { return (c.v & 8) ? 1 : 0; });
 }
 
 extern "C" int rans_gemv_rows2(const rans_w64_matrix* m, int x_dtype, int batch) {
@@ -1474,16 +1513,11 @@ extern "C" int rans_gemv_rows2(const rans_w64_matrix* m, int x_dtype, int batch)
     const size_t lds = (size_t)waves * wave_layout(m).raw_words * 2;
     const int ngroups = (m->cols / m->C) / waves;
     const int grid = (m->rows / m->R) * ngroups;
-    // the same per-chunk choices as launch_gemv_common: the table entries
-    // first (paired rows need the 8-byte ones), then the pairing
-    for (int B : {4, 1}) {
-        if ((B == 4 && batch < 2) || (B == 1 && batch % 4 != 1)) continue;
-        int v = var;
-        if ((m->flags & RANS_F_TABLE4 || m->table_lds4) && use_table4(m, B, var, waves, lds, grid))
-            v |= 8;
-        if (use_rows2(m, 1, v, waves, ngroups, grid, lds)) return 1;
-    }
-    return 0;
+    // the launches rans_w64_gemv makes (table entries first: paired rows
+    // need the 8-byte ones, then the pairing)
+    const bool t4_image = (m->flags & RANS_F_TABLE4) || m->table_lds4;
+    return plan_gemv(m, 1, var, waves, ngroups, lds, grid, batch, t4_image,
+                     [](const GemvChunk& c) { return (c.v & 16) ? 1 : 0; });
 }
 
 extern "C" int rans_w64_decode(const rans_w64_matrix* m, void* out_bf16, hipStream_t stream) {

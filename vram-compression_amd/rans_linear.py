@@ -2,7 +2,7 @@
 
 The reference names model integration as its next step (README.md:39) and
 stops at the kernel.  RansLinear is that step: forward(x) runs the fused
-decode+GEMV kernel for decode-sized batches (up to 8 rows) and, for larger
+decode+GEMV kernel for decode-sized batches (up to 8 or 16 rows) and, for larger
 batches (prefill), decodes the weight to bf16 once and calls the dense GEMM,
 which is then the faster path.  Inference only: the weight is not a
 parameter.
@@ -24,11 +24,11 @@ import torch
 
 import rans
 
-# Batches above this decode the weight to bf16 and use the dense GEMM.  The
-# fused GEMV runs 4 vectors per launch, so its time grows with the batch
-# while decode+GEMM stays flat; on MI355X the fused path wins up to 8 rows
-# on 1536x1536 to 25600x5120 matrices and loses from about 12.
-PREFILL_ROWS = 8
+# Batches above a matrix's fused_rows_limit decode the weight to bf16 and
+# use the dense GEMM.  The fused GEMV runs up to 8 vectors per launch (4
+# where tiles are taller than 8 rows), so its time grows with the batch
+# while decode+GEMM stays flat: on MI355X the fused path wins up to 16 rows
+# with the batch-8 kernel and up to 8 without it (RansMatrix.fused_rows_limit).
 
 
 def _entropy(codes):
@@ -82,7 +82,7 @@ class LinearGroup:
         if (self._x is not None and self._x() is x and self._version == x._version
                 and i in self._pending):
             return self._pending.pop(i)
-        if xd.shape[0] > PREFILL_ROWS:
+        if xd.shape[0] > self.members[0].matrix.fused_rows_limit:
             # all members decoded into row slices of one bf16 weight, one GEMM
             w = torch.empty(sum(m.out_features for m in self.members), xd.shape[1],
                             device="cuda", dtype=torch.bfloat16)
@@ -150,7 +150,7 @@ class RansLinear(torch.nn.Module):
             xd = xd.float()
         if self.group is not None:
             y = self.group.product(self, x, xd.contiguous())
-        elif xd.shape[0] > PREFILL_ROWS:
+        elif xd.shape[0] > self.matrix.fused_rows_limit:
             w = self.matrix.decode()  # bf16 code*step, then the dense GEMM
             y = torch.nn.functional.linear(xd.to(torch.bfloat16), w).float()
         else:
