@@ -535,13 +535,15 @@ def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False, batch=1):
 
 def configs():
     """The benchmark configurations beyond the headline shape: MLP shapes at
-    2.25 bits with 0.1% escapes, q_proj at 4.25 bits, the 27B-class shapes
+    2.25 bits with 0.1% escapes, q_proj at 4.25 bits, the headline shape at
+    batch 8 (one launch of the batch-8 kernel), the 27B-class shapes
     with Student-t codes and 1% escapes at batch 1 and 4, and the per-token
     196-GEMV chain with separate and with grouped launches.  Prints one JSON
     line per result."""
     lib = rans.build()
     cases = [
         ("q_proj 4.25b gauss", 1536, 1536, 4.25, "gauss", 0.0, 1),
+        ("1536x8960 3.25b laplace B8 (one batch-8 launch)", 1536, 8960, 3.25, "laplace", 0.0, 8),
         ("gate/up 2.25b esc0.1%", 8960, 1536, 2.25, "laplace", 0.001, 1),
         ("down 2.25b esc0.1%", 1536, 8960, 2.25, "laplace", 0.001, 1),
         ("27B 25600x5120 t3 2.25b esc1% B1", 25600, 5120, 2.25, "student3", 0.01, 1),
