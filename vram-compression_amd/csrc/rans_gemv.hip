@@ -27,6 +27,7 @@
 //      fixed order (no atomics on y, no memset, deterministic).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdint>
 #include <mutex>
@@ -945,32 +946,85 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
     }
 }
 
-// Fixed-rate 4-bit baseline, the reference's contract (rans_gemv.cu:107-131):
-// one wavefront per row, each lane reads 16 bytes (32 codes) per step.
-__global__ void __launch_bounds__(256) int4_gemv_kernel(const uint32_t* __restrict__ w,
-                                                        const float* __restrict__ x,
-                                                        float* __restrict__ y, int rows,
-                                                        int cols) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const uint4* wr = reinterpret_cast<const uint4*>(w + (int64_t)row * (cols / 8));
-    float acc = 0.f;
-    for (int j = lane; j < cols / 32; j += 64) {
-        const uint4 q = wr[j];
-        const uint32_t qs[4] = {q.x, q.y, q.z, q.w};
-        const float4* xp = reinterpret_cast<const float4*>(x + j * 32);
+// Fixed-rate baseline (rans_gemv.cu:107-131): eight biased nibbles per u32,
+// row-major, column 8j+b at bits 4b..4b+3, value = nibble - 8; y = W x' with
+// x' = x * step folded by the caller.  One workgroup of up to 8 waves (as
+// many as the row's 32-column blocks fill) takes ROWS rows: thread t takes
+// the blocks t, t + blockDim, ..., loads those 32 x' values once for all
+// its rows, and the waves' sums meet in LDS in a fixed order.  ROWS grows
+// with the matrix (2 to 16, about 1024 or more workgroups): few rows keep
+// small matrices' grids full, more rows stop large ones from reading x
+// once per pair of rows (34816x5120 in pairs: 356 MB of x reads against 89
+// MB of weights).  At 1536x8960 two rows measured fastest (rotated copies:
+// 5.8 us, against 6.7 with 4 rows, 8.9 with one row per 256-thread
+// workgroup, 12.2 with 8 rows, and 10.7 for one wave per row).  Nibbles
+// unpack four at a time: masked into the high half of each byte with bit 7
+// flipped, a byte holds 16 * (nibble - 8) as a signed 8-bit value, which
+// one sign-extending byte conversion reads; the total is scaled by 1/16 at
+// the end (exact).
+constexpr int kInt4MaxThreads = 512;
+
+__device__ __forceinline__ float int4_block_dot(uint32_t q, const float (&xs)[8]) {
+    // bytes of hi: 16*(n-8) of the odd nibbles (columns 1, 3, 5, 7); of lo:
+    // of the even ones (columns 0, 2, 4, 6)
+    const uint32_t hi = (q & 0xF0F0F0F0u) ^ 0x80808080u;
+    const uint32_t lo = ((q << 4) & 0xF0F0F0F0u) ^ 0x80808080u;
+    float a = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        a = fmaf((float)(int8_t)(lo >> (8 * k)), xs[2 * k], a);
+        a = fmaf((float)(int8_t)(hi >> (8 * k)), xs[2 * k + 1], a);
+    }
+    return a;
+}
+
+template <int ROWS>
+__global__ void __launch_bounds__(kInt4MaxThreads) int4_gemv_kernel(const uint32_t* __restrict__ w,
+                                                                    const float* __restrict__ x,
+                                                                    float* __restrict__ y, int rows,
+                                                                    int cols) {
+    constexpr int kInt4Rows = ROWS;
+    __shared__ float part[kInt4MaxThreads / 64][kInt4Rows];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nthr = blockDim.x;
+    const int row0 = blockIdx.x * kInt4Rows;
+    const int nblk = cols / 32;
+    const int64_t stride = cols / 8;  // u32 per row
+    // rows past the end re-read the last row and store nothing
+    const uint4* wr[kInt4Rows];
+#pragma unroll
+    for (int r = 0; r < kInt4Rows; r++)
+        wr[r] = reinterpret_cast<const uint4*>(w + (int64_t)min(row0 + r, rows - 1) * stride);
+    float acc[kInt4Rows];
+#pragma unroll
+    for (int r = 0; r < kInt4Rows; r++) acc[r] = 0.f;
+    for (int j = tid; j < nblk; j += nthr) {
+        const float4* xp = reinterpret_cast<const float4*>(x + (int64_t)j * 32);
+        float xs[4][8];
 #pragma unroll
         for (int a = 0; a < 4; a++) {
             const float4 x0 = xp[2 * a], x1 = xp[2 * a + 1];
-            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            xs[a][0] = x0.x; xs[a][1] = x0.y; xs[a][2] = x0.z; xs[a][3] = x0.w;
+            xs[a][4] = x1.x; xs[a][5] = x1.y; xs[a][6] = x1.z; xs[a][7] = x1.w;
+        }
 #pragma unroll
-            for (int b = 0; b < 8; b++)
-                acc = fmaf((float)((int)((qs[a] >> (4 * b)) & 15u) - 8), xs[b], acc);
+        for (int r = 0; r < kInt4Rows; r++) {
+            const uint4 q = wr[r][j];
+            acc[r] += int4_block_dot(q.x, xs[0]) + int4_block_dot(q.y, xs[1]) +
+                      int4_block_dot(q.z, xs[2]) + int4_block_dot(q.w, xs[3]);
         }
     }
-    acc = wave_sum63(acc);
-    if (lane == 63) y[row] = acc;
+#pragma unroll
+    for (int r = 0; r < kInt4Rows; r++) {
+        const float v = wave_sum63(acc[r]);
+        if (lane == 63) part[wave][r] = v;
+    }
+    __syncthreads();
+    if (tid < kInt4Rows && row0 + tid < rows) {
+        float v = 0.f;
+        for (int ww = 0; ww < nthr / 64; ww++) v += part[ww][tid];
+        y[row0 + tid] = v * 0.0625f;
+    }
 }
 
 // ------------------------------------------------------------------ host
@@ -1532,9 +1586,20 @@ extern "C" int launch_int4_gemv(const void* w, const void* x, void* y, int rows,
                                 hipStream_t stream) {
     if (!w || !x || !y || rows <= 0 || cols <= 0) return RANS_EARG;
     if (cols % 32) return RANS_EGEOMETRY;
-    hipLaunchKernelGGL(int4_gemv_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream,
-                       static_cast<const uint32_t*>(w), static_cast<const float*>(x),
-                       static_cast<float*>(y), rows, cols);
+    // one wave per 64 column blocks, at most 8; rows per workgroup: the
+    // largest of 2, 4, 8, 16 that leaves at least 1024 workgroups (2 below)
+    const int waves = std::min(kInt4MaxThreads / 64, (cols / 32 + 63) / 64);
+    const int nr = rows >= 16 * 1024 ? 16 : rows >= 8 * 1024 ? 8 : rows >= 4 * 1024 ? 4 : 2;
+    const auto* wp = static_cast<const uint32_t*>(w);
+    const auto* xp = static_cast<const float*>(x);
+    auto* yp = static_cast<float*>(y);
+    const dim3 grid((rows + nr - 1) / nr), block(64 * waves);
+    switch (nr) {
+        case 16: hipLaunchKernelGGL(int4_gemv_kernel<16>, grid, block, 0, stream, wp, xp, yp, rows, cols); break;
+        case 8: hipLaunchKernelGGL(int4_gemv_kernel<8>, grid, block, 0, stream, wp, xp, yp, rows, cols); break;
+        case 4: hipLaunchKernelGGL(int4_gemv_kernel<4>, grid, block, 0, stream, wp, xp, yp, rows, cols); break;
+        default: hipLaunchKernelGGL(int4_gemv_kernel<2>, grid, block, 0, stream, wp, xp, yp, rows, cols); break;
+    }
     return (int)hipGetLastError();
 }
 
