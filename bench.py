@@ -336,25 +336,35 @@ def main():
                    "hot_us_per_gemv": tb_hot, "copies": nW,
                    "rotation": rotation_record(args.steps, nW, ROWS * COLS * 2),
                    "speedup_rans_vs_bf16": tb_rot / t_rot}
-        del Ws, fns
+        # the library's own bf16 GEMV on the same copies: what an uncompressed
+        # GEMV reaches near the HBM bound
+        mbs = [rans.Bf16Matrix(Wd, lib) for Wd in Ws]
+        yb16 = torch.empty(ROWS, device="cuda")
+        th_rot = graph_time_us([lambda mb=mb: mb.gemv(xb, yb16) for mb in mbs], args.steps,
+                               args.warmup, rotate=nW)
+        rocblas["bf16_hip_us_per_gemv"] = th_rot
+        rocblas["bf16_hip_GBps"] = ROWS * COLS * 2 / th_rot / 1e3
+        rocblas["speedup_rans_vs_bf16_hip"] = th_rot / t_rot
+        del Ws, fns, mbs
         # the reference's other comparators (kernel/bench.py:97-111): the
         # fixed-rate int4 GEMV (host fold + int4 kernel) and decode-to-bf16
         # followed by the bf16 GEMV
         n4 = copies_for(args.steps, ROWS * COLS // 2)
-        m4s = [rans.Int4Matrix(np.clip(codes, -8, 7), step_t, lib) for _ in range(n4)]
+        m4 = rans.Int4Matrix(np.clip(codes, -8, 7), step_t, lib)
+        m4s = [m4] + [m4.clone() for _ in range(n4 - 1)]
         xf = xb.float()
         y4 = torch.empty(ROWS, device="cuda")
         rocblas["int4_us_per_gemv"] = graph_time_us([lambda m4=m4: m4.gemv(xf, y4) for m4 in m4s],
                                                     args.steps, args.warmup, rotate=n4)
-        del m4s
+        del m4s, m4
         m = rans.RansMatrix(enc, step_t, lib)
         buf = torch.empty(ROWS, COLS, device="cuda", dtype=torch.bfloat16)
         rocblas["decode_then_bf16_us_per_gemv"] = graph_time_us(
             [lambda: torch.nn.functional.linear(xb, m.decode(buf))], 50, args.warmup)
         del m, buf
         torch.cuda.empty_cache()
-        print(f"bf16 F.linear: {tb_rot:.2f} us rotated, {tb_hot:.2f} us hot", file=sys.stderr,
-              flush=True)
+        print(f"bf16 F.linear: {tb_rot:.2f} us rotated, {tb_hot:.2f} us hot; "
+              f"bf16 HIP GEMV: {th_rot:.2f} us rotated", file=sys.stderr, flush=True)
 
     # The same matrix in the reference's own 32-lane layout at its published
     # tiling of this shape (R=8, C=8960: 6144 streams of 2240 symbols,

@@ -200,6 +200,15 @@ int rans_w64_decode_codes(const rans_w64_matrix* m, int32_t* out, hipStream_t st
 int launch_int4_gemv(const void* w, const void* x, void* y, int rows, int cols,
                      hipStream_t stream);
 
+/* Dense bf16 GEMV comparator: y[r] = sum_c W[r,c] * x[c] with W rows x cols
+ * bf16 row-major, x bf16, y f32 (f32 accumulation).  The reference times this
+ * product through torch's F.linear (bench.py:96); this is the uncompressed
+ * HBM-bound GEMV written like the others here, so the compressed kernels are
+ * also compared against a bf16 GEMV that runs near the HBM bound.  cols % 8
+ * == 0 and w, x 16-byte aligned, else RANS_EGEOMETRY; RANS_EARG for null
+ * pointers or non-positive sizes. */
+int bf16_gemv(const void* w, const void* x, void* y, int rows, int cols, hipStream_t stream);
+
 /* The reference's two rANS entry points, with its argument lists and stream
  * format (rans_gemv.cu:146-162, bound by kernel/rans.py:25-29 as
  * [c_int] + [c_void_p]*5 + [c_int]*3 + [c_void_p]): words / offs / table as

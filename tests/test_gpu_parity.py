@@ -202,15 +202,40 @@ def test_graph_replay_matches_eager(rans, oracle, lib, dev):
             torch.cuda.synchronize()
 
 
-def test_int4_baseline(rans, lib, dev):
-    print("case int4", flush=True)
-    codes = np.random.default_rng(1).integers(-8, 8, size=(256, 1024))
-    step = torch.rand(1024) + 0.5
+# rows x cols: the int4 kernel's 4-row workgroups of 1 and 8 waves and its
+# 8-row workgroups of 4 waves (both dimensions from 4096), row counts not
+# multiples of them, blocks per row that leave a one-block tail (17, 33, 65)
+# or run the two-block loop (1088; 257 = one pair and a tail)
+@pytest.mark.parametrize("rows,cols", [(256, 1024), (4099, 1056), (8200, 2080), (16390, 544),
+                                       (300, 34816), (4097, 8224)])
+def test_int4_baseline(rans, lib, dev, rows, cols):
+    print(f"case int4 {rows}x{cols}", flush=True)
+    codes = np.random.default_rng(rows).integers(-8, 8, size=(rows, cols))
+    step = torch.rand(cols) + 0.5
     m4 = rans.Int4Matrix(codes, step, lib)
-    x = torch.randn(1024, device="cuda")
+    x = torch.randn(cols, device="cuda")
     y_ref = torch.from_numpy(codes).double().cuda() @ (x.double() * step.double().cuda())
     y = m4.gemv(x)
     assert torch.allclose(y.double(), y_ref, rtol=1e-4, atol=1e-3)
+
+
+# rows x cols: odd row counts (the last two-row workgroup has one row),
+# 16-byte chunk counts that take 1 to 8 waves, leave a one-chunk tail or run
+# several passes of 8 waves; the 1536x8960 headline shape
+@pytest.mark.parametrize("rows,cols", [(7, 136), (2049, 1544), (4100, 5120), (8197, 17408),
+                                       (1536, 8960)])
+def test_bf16_comparator(rans, lib, dev, rows, cols):
+    """The dense bf16 GEMV against float64 of the same bf16 values (f32
+    accumulation: relative L2 within 1e-5)."""
+    print(f"case bf16 gemv {rows}x{cols}", flush=True)
+    g = torch.Generator().manual_seed(rows)
+    W = torch.randn(rows, cols, generator=g).bfloat16()
+    x = torch.randn(cols, generator=g).bfloat16()
+    mb = rans.Bf16Matrix(W, lib)
+    y = mb.gemv(x.cuda())
+    y_ref = W.double() @ x.double()
+    err = (torch.linalg.vector_norm(y.cpu().double() - y_ref) / torch.linalg.vector_norm(y_ref)).item()
+    assert err < 1e-5, err
 
 
 @pytest.mark.parametrize("R,C,S", [(4, 256, 1), (8, 512, 2), (16, 128, 1), (2, 256, 4)])

@@ -948,21 +948,40 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
 
 // Fixed-rate baseline (rans_gemv.cu:107-131): eight biased nibbles per u32,
 // row-major, column 8j+b at bits 4b..4b+3, value = nibble - 8; y = W x' with
-// x' = x * step folded by the caller.  One workgroup of up to 8 waves (as
-// many as the row's 32-column blocks fill) takes ROWS rows: thread t takes
-// the blocks t, t + blockDim, ..., loads those 32 x' values once for all
-// its rows, and the waves' sums meet in LDS in a fixed order.  ROWS grows
-// with the matrix (2 to 16, about 1024 or more workgroups): few rows keep
-// small matrices' grids full, more rows stop large ones from reading x
-// once per pair of rows (34816x5120 in pairs: 356 MB of x reads against 89
-// MB of weights).  At 1536x8960 two rows measured fastest (rotated copies:
-// 5.8 us, against 6.7 with 4 rows, 8.9 with one row per 256-thread
-// workgroup, 12.2 with 8 rows, and 10.7 for one wave per row).  Nibbles
-// unpack four at a time: masked into the high half of each byte with bit 7
+// x' = x * step folded by the caller.  A workgroup takes ROWS rows: thread t
+// takes the 32-column blocks t, t + blockDim, ..., two blocks per row in
+// flight per iteration, loads the 32 x' values of a block once for all its
+// rows, and the waves' sums meet in LDS in a fixed order.  Launch shape, from
+// a sweep of 1 to 16 rows per workgroup, 1 to 8 waves and one or two blocks
+// in flight over the benchmark shapes (rotated copies, us): 8 rows and 4
+// waves where both dimensions reach 4096 (25600x5120: 19.9, against 24.0 for
+// 16 rows and one block in flight; 5120x17408: 17.8; 5120x5120: 7.2), else
+// 4 rows and 8 waves (1536x8960: 5.7), and one wave where a row has at most
+// 64 blocks (17920x1536: 6.8, against 13.5 for 16 rows).  Nibbles unpack
+// four at a time: masked into the high half of each byte with bit 7
 // flipped, a byte holds 16 * (nibble - 8) as a signed 8-bit value, which
 // one sign-extending byte conversion reads; the total is scaled by 1/16 at
 // the end (exact).
 constexpr int kInt4MaxThreads = 512;
+
+// Marks loaded registers as used here: every load above is issued before
+// anything after waits for one.  (A memory clobber does not do this for
+// const __restrict__ pointers: the compiler may still defer their loads to
+// first use, and then waits for each in turn.)
+__device__ __forceinline__ void pin(uint4& v) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // one 128-bit operand
+    u32x4 t = __builtin_bit_cast(u32x4, v);
+    asm volatile("" : "+v"(t));
+    v = __builtin_bit_cast(uint4, t);
+}
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+template <int N>
+__device__ __forceinline__ void pin(float (&v)[4][N]) {
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int k = 0; k < N; k++) pin(v[a][k]);
+}
 
 __device__ __forceinline__ float int4_block_dot(uint32_t q, const float (&xs)[8]) {
     // bytes of hi: 16*(n-8) of the odd nibbles (columns 1, 3, 5, 7); of lo:
@@ -978,52 +997,187 @@ __device__ __forceinline__ float int4_block_dot(uint32_t q, const float (&xs)[8]
     return a;
 }
 
+// x' of 32-column block j
+__device__ __forceinline__ void int4_load_x(const float* __restrict__ x, int j, float (&xs)[4][8]) {
+    const float4* xp = reinterpret_cast<const float4*>(x + (int64_t)j * 32);
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const float4 x0 = xp[2 * a], x1 = xp[2 * a + 1];
+        xs[a][0] = x0.x; xs[a][1] = x0.y; xs[a][2] = x0.z; xs[a][3] = x0.w;
+        xs[a][4] = x1.x; xs[a][5] = x1.y; xs[a][6] = x1.z; xs[a][7] = x1.w;
+    }
+}
+
+__device__ __forceinline__ float int4_dot(const uint4 q, const float (&xs)[4][8]) {
+    return int4_block_dot(q.x, xs[0]) + int4_block_dot(q.y, xs[1]) + int4_block_dot(q.z, xs[2]) +
+           int4_block_dot(q.w, xs[3]);
+}
+
 template <int ROWS>
 __global__ void __launch_bounds__(kInt4MaxThreads) int4_gemv_kernel(const uint32_t* __restrict__ w,
                                                                     const float* __restrict__ x,
                                                                     float* __restrict__ y, int rows,
                                                                     int cols) {
-    constexpr int kInt4Rows = ROWS;
-    __shared__ float part[kInt4MaxThreads / 64][kInt4Rows];
+    __shared__ float part[kInt4MaxThreads / 64][ROWS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nthr = blockDim.x;
-    const int row0 = blockIdx.x * kInt4Rows;
+    const int row0 = blockIdx.x * ROWS;
     const int nblk = cols / 32;
     const int64_t stride = cols / 8;  // u32 per row
     // rows past the end re-read the last row and store nothing
-    const uint4* wr[kInt4Rows];
+    const uint4* wr[ROWS];
 #pragma unroll
-    for (int r = 0; r < kInt4Rows; r++)
+    for (int r = 0; r < ROWS; r++)
         wr[r] = reinterpret_cast<const uint4*>(w + (int64_t)min(row0 + r, rows - 1) * stride);
-    float acc[kInt4Rows];
+    float acc[ROWS];
 #pragma unroll
-    for (int r = 0; r < kInt4Rows; r++) acc[r] = 0.f;
-    for (int j = tid; j < nblk; j += nthr) {
-        const float4* xp = reinterpret_cast<const float4*>(x + (int64_t)j * 32);
+    for (int r = 0; r < ROWS; r++) acc[r] = 0.f;
+    int j = tid;
+    for (; j + nthr < nblk; j += 2 * nthr) {
+        uint4 q0[ROWS], q1[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) {
+            q0[r] = wr[r][j];
+            q1[r] = wr[r][j + nthr];
+        }
+        float xs[4][8], xt[4][8];
+        int4_load_x(x, j, xs);
+        int4_load_x(x, j + nthr, xt);
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) {
+            pin(q0[r]);
+            pin(q1[r]);
+        }
+        pin(xs);
+        pin(xt);
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) acc[r] += int4_dot(q0[r], xs) + int4_dot(q1[r], xt);
+    }
+    if (j < nblk) {
+        // every row's block requested before the first is used: left to
+        // itself the compiler issues two and then waits for each of the
+        // others in turn (34816x5120: 33.5 against 25.6 us)
+        uint4 q[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) q[r] = wr[r][j];
         float xs[4][8];
+        int4_load_x(x, j, xs);
 #pragma unroll
-        for (int a = 0; a < 4; a++) {
-            const float4 x0 = xp[2 * a], x1 = xp[2 * a + 1];
-            xs[a][0] = x0.x; xs[a][1] = x0.y; xs[a][2] = x0.z; xs[a][3] = x0.w;
-            xs[a][4] = x1.x; xs[a][5] = x1.y; xs[a][6] = x1.z; xs[a][7] = x1.w;
-        }
+        for (int r = 0; r < ROWS; r++) pin(q[r]);
+        pin(xs);
 #pragma unroll
-        for (int r = 0; r < kInt4Rows; r++) {
-            const uint4 q = wr[r][j];
-            acc[r] += int4_block_dot(q.x, xs[0]) + int4_block_dot(q.y, xs[1]) +
-                      int4_block_dot(q.z, xs[2]) + int4_block_dot(q.w, xs[3]);
-        }
+        for (int r = 0; r < ROWS; r++) acc[r] += int4_dot(q[r], xs);
     }
 #pragma unroll
-    for (int r = 0; r < kInt4Rows; r++) {
+    for (int r = 0; r < ROWS; r++) {
         const float v = wave_sum63(acc[r]);
         if (lane == 63) part[wave][r] = v;
     }
     __syncthreads();
-    if (tid < kInt4Rows && row0 + tid < rows) {
+    if (tid < ROWS && row0 + tid < rows) {
         float v = 0.f;
         for (int ww = 0; ww < nthr / 64; ww++) v += part[ww][tid];
         y[row0 + tid] = v * 0.0625f;
+    }
+}
+
+// Dense bf16 GEMV, the uncompressed comparator: y = W x with W rows x cols
+// bf16 row-major, x bf16, y f32 (f32 accumulation), the product F.linear
+// computes (bench.py:96 times it through the BLAS library).  A workgroup of
+// up to 8 waves takes two rows: thread t takes the 16-byte column chunks t,
+// t + blockDim, ..., two chunks per row in flight per iteration, each chunk
+// of x (8 values) unpacked once for both rows; the waves' sums meet in LDS
+// in a fixed order.  A bf16 value is the high half of its f32, so unpacking
+// is a shift or a mask.  Measured over 1 to 8 rows per workgroup, 2 to 16
+// waves and 1 to 4 chunks in flight on the benchmark shapes, two rows with
+// one wave per 64 chunks (at most 8) and two chunks in flight was the
+// fastest or within 5% of it on each (25600x5120: 40 us, 6.5 TB/s; the
+// same kernel with 8 rows per workgroup took 51).
+constexpr int kBf16MaxThreads = 512;
+constexpr int kBf16Rows = 2;
+
+__device__ __forceinline__ float bf16_chunk_dot(const uint4 q, const float (&xs)[8], float a) {
+    const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        a = fmaf(__uint_as_float(u[k] << 16), xs[2 * k], a);
+        a = fmaf(__uint_as_float(u[k] & 0xFFFF0000u), xs[2 * k + 1], a);
+    }
+    return a;
+}
+
+__device__ __forceinline__ void bf16_unpack8(const uint4 v, float (&xs)[8]) {
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        xs[2 * k] = __uint_as_float(u[k] << 16);
+        xs[2 * k + 1] = __uint_as_float(u[k] & 0xFFFF0000u);
+    }
+}
+
+__global__ void __launch_bounds__(kBf16MaxThreads) bf16_gemv_kernel(const uint4* __restrict__ w,
+                                                                    const uint4* __restrict__ x,
+                                                                    float* __restrict__ y,
+                                                                    int rows, int cols) {
+    constexpr int ROWS = kBf16Rows;
+    __shared__ float part[kBf16MaxThreads / 64][ROWS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nthr = blockDim.x;
+    const int row0 = blockIdx.x * ROWS;
+    const int nchunk = cols / 8;  // 16-byte chunks per row
+    // rows past the end re-read the last row and store nothing
+    const uint4* wr[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) wr[r] = w + (int64_t)min(row0 + r, rows - 1) * nchunk;
+    float acc[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) acc[r] = 0.f;
+    int j = tid;
+    for (; j + nthr < nchunk; j += 2 * nthr) {
+        uint4 q0[ROWS], q1[ROWS];
+        uint4 x0 = x[j], x1 = x[j + nthr];
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) {
+            q0[r] = wr[r][j];
+            q1[r] = wr[r][j + nthr];
+        }
+        // all loads requested before the first use
+        pin(x0);
+        pin(x1);
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) {
+            pin(q0[r]);
+            pin(q1[r]);
+        }
+        float xs0[8], xs1[8];
+        bf16_unpack8(x0, xs0);
+        bf16_unpack8(x1, xs1);
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) acc[r] = bf16_chunk_dot(q1[r], xs1, bf16_chunk_dot(q0[r], xs0, acc[r]));
+    }
+    if (j < nchunk) {
+        uint4 q[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) q[r] = wr[r][j];
+        uint4 xv = x[j];
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) pin(q[r]);
+        pin(xv);
+        float xs[8];
+        bf16_unpack8(xv, xs);
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) acc[r] = bf16_chunk_dot(q[r], xs, acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) {
+        const float v = wave_sum63(acc[r]);
+        if (lane == 63) part[wave][r] = v;
+    }
+    __syncthreads();
+    if (tid < ROWS && row0 + tid < rows) {
+        float v = 0.f;
+        for (int ww = 0; ww < nthr / 64; ww++) v += part[ww][tid];
+        y[row0 + tid] = v;
     }
 }
 
@@ -1586,20 +1740,31 @@ extern "C" int launch_int4_gemv(const void* w, const void* x, void* y, int rows,
                                 hipStream_t stream) {
     if (!w || !x || !y || rows <= 0 || cols <= 0) return RANS_EARG;
     if (cols % 32) return RANS_EGEOMETRY;
-    // one wave per 64 column blocks, at most 8; rows per workgroup: the
-    // largest of 2, 4, 8, 16 that leaves at least 1024 workgroups (2 below)
-    const int waves = std::min(kInt4MaxThreads / 64, (cols / 32 + 63) / 64);
-    const int nr = rows >= 16 * 1024 ? 16 : rows >= 8 * 1024 ? 8 : rows >= 4 * 1024 ? 4 : 2;
+    // rows per workgroup and waves as measured (see the kernel)
+    const int nblk = cols / 32;
+    const bool large = rows >= 4096 && cols >= 4096;
+    const int waves = nblk <= 64 ? 1 : large ? 4 : 8;
     const auto* wp = static_cast<const uint32_t*>(w);
     const auto* xp = static_cast<const float*>(x);
     auto* yp = static_cast<float*>(y);
-    const dim3 grid((rows + nr - 1) / nr), block(64 * waves);
-    switch (nr) {
-        case 16: hipLaunchKernelGGL(int4_gemv_kernel<16>, grid, block, 0, stream, wp, xp, yp, rows, cols); break;
-        case 8: hipLaunchKernelGGL(int4_gemv_kernel<8>, grid, block, 0, stream, wp, xp, yp, rows, cols); break;
-        case 4: hipLaunchKernelGGL(int4_gemv_kernel<4>, grid, block, 0, stream, wp, xp, yp, rows, cols); break;
-        default: hipLaunchKernelGGL(int4_gemv_kernel<2>, grid, block, 0, stream, wp, xp, yp, rows, cols); break;
-    }
+    const dim3 block(64 * waves);
+    if (large)
+        hipLaunchKernelGGL(int4_gemv_kernel<8>, dim3((rows + 7) / 8), block, 0, stream, wp, xp, yp, rows, cols);
+    else
+        hipLaunchKernelGGL(int4_gemv_kernel<4>, dim3((rows + 3) / 4), block, 0, stream, wp, xp, yp, rows, cols);
+    return (int)hipGetLastError();
+}
+
+extern "C" int bf16_gemv(const void* w, const void* x, void* y, int rows, int cols,
+                         hipStream_t stream) {
+    if (!w || !x || !y || rows <= 0 || cols <= 0) return RANS_EARG;
+    if (cols % 8 || ((uintptr_t)w | (uintptr_t)x) % 16) return RANS_EGEOMETRY;
+    // one wave per 64 chunks of a row, at most 8; two rows per workgroup
+    const int nchunk = cols / 8;
+    const int waves = std::min(kBf16MaxThreads / 64, (nchunk + 63) / 64);
+    const dim3 grid((rows + kBf16Rows - 1) / kBf16Rows), block(64 * waves);
+    hipLaunchKernelGGL(bf16_gemv_kernel, grid, block, 0, stream, static_cast<const uint4*>(w),
+                       static_cast<const uint4*>(x), static_cast<float*>(y), rows, cols);
     return (int)hipGetLastError();
 }
 

@@ -255,10 +255,15 @@ def bench(rotate_bytes=512 << 20, iters=200):
             nW = max(1, -(-rotate_bytes // (rows * cols * 2)))
             Ws = [(torch.from_numpy(codes).float() * step).bfloat16().cuda() for _ in range(nW)]
             t_bf16 = timeit_graph([lambda W=W: torch.nn.functional.linear(xb, W) for W in Ws], iters)
-            del Ws
+            mbs = [rans.Bf16Matrix(W, lib) for W in Ws]
+            yh = torch.empty(rows, device="cuda")
+            t_bf16_hip = timeit_graph([lambda mb=mb: mb.gemv(xb, yh) for mb in mbs], iters)
+            del Ws, mbs
+            n4 = max(1, -(-rotate_bytes // (rows * cols // 2)))
             m4 = rans.Int4Matrix(np.clip(codes, -8, 7), step, lib)
+            m4s = [m4] + [m4.clone() for _ in range(n4 - 1)]
             y4 = torch.empty(rows, device="cuda")
-            t_int4 = timeit_graph(lambda: m4.gemv(x, y4), iters)
+            t_int4 = timeit_graph([lambda m4=m4: m4.gemv(x, y4) for m4 in m4s], iters)
             best = None
             for S in (1, 2):
                 R, C = pick_tiling(rows, cols, S=S)
@@ -277,13 +282,14 @@ def bench(rotate_bytes=512 << 20, iters=200):
                                 bits_overhead=enc["bits_state_offs"] + enc["bits_table"] + enc["bits_escape"])
                 del ms, m
             r = dict(shape=name, rows=rows, cols=cols, entropy=entropy_fast(codes),
-                     t_bf16_us=t_bf16, t_int4_us=t_int4, **best)
+                     t_bf16_us=t_bf16, t_bf16_hip_us=t_bf16_hip, t_int4_us=t_int4, **best)
             r["speedup_vs_bf16"] = t_bf16 / r["t_rans_us"]
+            r["speedup_vs_bf16_hip"] = t_bf16_hip / r["t_rans_us"]
             r["speedup_vs_int4"] = t_int4 / r["t_rans_us"]
             print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}),
                   flush=True)
             out.append(r)
-            del m4
+            del m4s, m4
             torch.cuda.empty_cache()
     os.makedirs(RES, exist_ok=True)
     with open(os.path.join(RES, "kernel_bench.json"), "w") as f:
