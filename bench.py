@@ -78,9 +78,10 @@ def graph_time_us(fns, steps, warmup, rotate=None):
     rotate (the number of copies the calls in fns rotate over, len(fns)):
     when steps is smaller than that, the timed graph runs calls 0..steps-1
     and a second, untimed graph runs all the others just before the timed
-    replay, so every timed call reads a copy that at least 512 MiB of other
-    copies have displaced from the 256 MB Infinity Cache and the L2 since
-    its last read; otherwise the timed calls cycle through all copies."""
+    replay; otherwise the timed calls cycle through all copies, after an
+    untimed pass over every copy in order.  Either way every timed call
+    reads a copy that at least 512 MiB of other copies have displaced from
+    the 256 MB Infinity Cache and the L2 since its last read."""
     n = len(fns)
     for i in range(warmup):
         fns[i % n]()
@@ -95,16 +96,26 @@ def graph_time_us(fns, steps, warmup, rotate=None):
     with torch.cuda.graph(g):
         for i in range(steps):
             fns[i % n]()
-    flush = None
-    if rotate and steps < n:
-        flush = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(flush):
-            for i in range(steps, n):
-                fns[i]()
+    # Untimed lead-in replayed just before the timed graph: when rotating,
+    # the copies the timed launches do not use (steps < n) or every copy
+    # once in order (steps >= n), so each timed launch reads a copy that at
+    # least 512 MiB of other copies followed; else the timed graph itself.
+    lead = None
+    if rotate:
+        lead = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(lead):
+            for f in (fns[steps:] if steps < n else fns):
+                f()
     g.replay()  # untimed: first replay uploads the graph
-    if flush is not None:
-        flush.replay()
+    if lead is not None:
+        lead.replay()
     torch.cuda.synchronize()
+    # The timed replay is queued while the device still runs the lead-in, so
+    # the start event fires when that work ends and not while the host is
+    # still submitting the timed graph: the events time the device's `steps`
+    # launches.  With the device idle at the start event, 20 launches of the
+    # 1536x8960 GEMV read 0.5-0.9 us per launch above their kernel time.
+    (lead if lead is not None else g).replay()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     g.replay()
@@ -400,6 +411,7 @@ def main():
     if not args.no_chain:
         r = B.chain(grouped=True)
         chain = {"us_per_token": r["t_rans_us"], "bf16_us_per_token": r["t_bf16_us"],
+                 "bf16_hip_us_per_token": r["t_bf16_hip_us"],
                  "speedup_vs_bf16": r["speedup_vs_bf16"], "launches": r["launches"],
                  "gemvs": r["gemvs"], "bits_total": r["bits_total"],
                  "workload": r["config"]}

@@ -196,7 +196,8 @@ int rans_w64_decode_codes(const rans_w64_matrix* m, int32_t* out, hipStream_t st
 
 /* Fixed-rate 4-bit baseline GEMV, same contract as the reference
  * (rans_gemv.cu:164-170): w packs 8 codes per u32 (nibble b of word j of row
- * r is column 8j+b, value nibble-8), x is the host-folded f32 x*step, y f32. */
+ * r is column 8j+b, value nibble-8), x is the host-folded f32 x*step, y f32.
+ * cols % 32 == 0 and w, x 16-byte aligned, else RANS_EGEOMETRY. */
 int launch_int4_gemv(const void* w, const void* x, void* y, int rows, int cols,
                      hipStream_t stream);
 

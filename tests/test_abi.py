@@ -91,6 +91,7 @@ def test_argument_validation_without_gpu(rans, lib):
     assert lib.rans_w64_decode_codes(ctypes.byref(d), None, None) == -4
     assert lib.launch_int4_gemv(None, x, y, 4, 64, None) == -4
     assert lib.launch_int4_gemv(x, x, y, 4, 48, None) == -2
+    assert lib.launch_int4_gemv(x, ctypes.c_void_p(0x2004), y, 4, 64, None) == -2  # x not 16-byte aligned
     assert lib.bf16_gemv(None, x, y, 4, 64, None) == -4
     assert lib.bf16_gemv(x, x, y, 0, 64, None) == -4
     assert lib.bf16_gemv(x, x, y, 4, 60, None) == -2  # cols not a multiple of 8

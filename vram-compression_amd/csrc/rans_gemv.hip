@@ -1739,7 +1739,8 @@ extern "C" int rans_w64_decode_codes(const rans_w64_matrix* m, int32_t* out, hip
 extern "C" int launch_int4_gemv(const void* w, const void* x, void* y, int rows, int cols,
                                 hipStream_t stream) {
     if (!w || !x || !y || rows <= 0 || cols <= 0) return RANS_EARG;
-    if (cols % 32) return RANS_EGEOMETRY;
+    // 16-byte loads of w rows and x blocks
+    if (cols % 32 || ((uintptr_t)w | (uintptr_t)x) % 16) return RANS_EGEOMETRY;
     // rows per workgroup and waves as measured (see the kernel)
     const int nblk = cols / 32;
     const bool large = rows >= 4096 && cols >= 4096;

@@ -162,13 +162,14 @@ def copies_for(iters, nbytes, rotate_bytes=512 << 20):
 
 
 def timeit_graph(fns, iters=200, warmup=10, rotate=False):
-    """Device time per call: fns (one callable, or a list cycled through, e.g.
-    one per rotating copy) are captured `iters` times in a HIP graph; the
-    graph is replayed once untimed and then timed between HIP events.
-    rotate (fns sized by copies_for): when iters is below len(fns), the timed
-    graph runs calls 0..iters-1 and an untimed graph of all the other calls
-    runs just before the timed replay, so every timed call reads a copy that
-    the other copies have displaced from the caches.
+    """Device time per call: fns (one callable, or a list cycled through, one
+    per rotating copy, sized by copies_for) are captured `iters` times in a
+    HIP graph; the graph is replayed once untimed and then timed between HIP
+    events.  With several copies, an untimed graph runs just before the
+    timed replay: the copies the timed graph does not use (iters below
+    len(fns)), else every copy once in order, so every timed call reads a
+    copy that the other copies have displaced from the caches.  rotate is
+    accepted for older callers and has no further effect.
     Returns microseconds per call."""
     if callable(fns):
         fns = [fns]
@@ -186,16 +187,22 @@ def timeit_graph(fns, iters=200, warmup=10, rotate=False):
     with torch.cuda.graph(g):
         for i in range(iters):
             fns[i % len(fns)]()
-    flush = None
-    if rotate and iters < len(fns):
-        flush = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(flush):
-            for f in fns[iters:]:
+    # untimed lead-in replayed just before the timed graph: with several
+    # copies, the ones the timed calls do not use (iters < len(fns)) or every
+    # copy once in order, so each timed call reads a copy all the others
+    # followed; with one callable, the timed graph once more
+    lead = g
+    if len(fns) > 1:
+        lead = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(lead):
+            for f in (fns[iters:] if iters < len(fns) else fns):
                 f()
     g.replay()
-    if flush is not None:
-        flush.replay()
+    lead.replay()
     torch.cuda.synchronize()
+    # queued behind the lead-in, so the start event does not wait for the
+    # host to submit the timed graph
+    lead.replay()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     g.replay()
@@ -497,8 +504,9 @@ def run_chain(ch, ys):
 def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False, batch=1):
     """Per-token chain of 7*layers batch-1 GEMVs over a random-init
     Qwen2.5-1.5B-shaped weight set (build_chain), graph-captured and
-    replayed; the same chain with bf16 F.linear.  Returns the total
-    weight-pass latency of both.
+    replayed; the same chain with bf16 F.linear and, at batch 1, with the
+    library's dense bf16_gemv.  Returns the total weight-pass latency of
+    each.
 
     grouped: q, k, v and gate, up of a layer each run as one grouped launch
     (gemv_group, tiled with pick_group_tiling); the bf16 chain then runs q, k,
@@ -530,12 +538,27 @@ def chain(bits=3.25, layers=28, seed=0, iters=3, grouped=False, batch=1):
 
     t_rans = timeit_graph(lambda: run_chain(ch, ys), iters, warmup=2)
     t_bf16 = timeit_graph(run_bf16, iters, warmup=2)
+    # the same bf16 weights through the library's dense bf16_gemv (batch 1)
+    t_bf16_hip = None
+    if batch == 1:
+        mbs = [rans.Bf16Matrix(W, mats[0].lib) for W in Ws]
+        yh = {}
+        for mb in mbs:
+            yh.setdefault(mb.rows, torch.empty(mb.rows, device="cuda"))
+
+        def run_bf16_hip():
+            for mb in mbs:
+                mb.gemv(xs[mb.cols][0], yh[mb.rows])
+
+        t_bf16_hip = timeit_graph(run_bf16_hip, iters, warmup=2)
+        del mbs
     nweights, nbytes = ch["nweights"], ch["nbytes"]
     return dict(config=f"Qwen2.5-1.5B-shaped weight set, {layers} layers x 7 matrices, "
                 f"batch {batch}" + (", q/k/v and gate/up grouped" if grouped else ""),
                 gemvs=len(mats), launches=len(ch["launches"]), weights=nweights,
                 bits_target=bits, bits_total=8 * nbytes / nweights, compressed_MB=nbytes / 1e6,
                 bf16_MB=nweights * 2 / 1e6, t_rans_us=t_rans, t_bf16_us=t_bf16,
+                t_bf16_hip_us=t_bf16_hip,
                 effective_GBps=nweights * 2 / t_rans / 1e3, speedup_vs_bf16=t_bf16 / t_rans)
 
 
