@@ -369,8 +369,9 @@ def chain_tiling(rows, cols):
 
 def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None, C=None, S=1,
                   iters=100, rotate_bytes=512 << 20, codes=None, step=None):
-    """Times one encoded matrix (rotated over >= rotate_bytes of copies) and
-    the bf16 F.linear on the same shape and rotation; checks the GEMV.
+    """Times one encoded matrix (rotated over >= rotate_bytes of copies),
+    the bf16 F.linear and the library's bf16_gemv on the same shape and
+    rotation; checks the GEMV.
     codes/step: a given matrix and its steps instead of synthetic ones."""
     if codes is None:
         codes = synth_codes_full(rows, cols, bits, dist=dist, seed=seed, escape_frac=escape_frac)
@@ -392,6 +393,17 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
     Ws = [W] + [W.clone() for _ in range(nW - 1)]
     t_bf16 = timeit_graph([lambda Wd=Wd: torch.nn.functional.linear(x, Wd) for Wd in Ws], iters,
                           rotate=True)
+    # the library's dense bf16_gemv on the same copies (one vector per launch,
+    # so batch b takes b launches)
+    mbs = [rans.Bf16Matrix(Wd, lib) for Wd in Ws]
+    yh = torch.empty(rows, device="cuda")
+
+    def dense(mb):
+        for b in range(batch):
+            mb.gemv(x[b], yh)
+
+    t_bf16_hip = timeit_graph([lambda mb=mb: dense(mb) for mb in mbs], iters, rotate=True)
+    del mbs
     # against the exact product codes @ (x * step) in float64 (the bf16
     # comparator's weights are themselves rounded)
     ref = (x.double() * step.double().cuda()) @ torch.from_numpy(codes).cuda().double().t()
@@ -401,7 +413,7 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
                batch=batch, R=R, C=C, S=S, word_fetch={1: "always", 2: "refill"}[flags & 3],
                entropy=entropy_fast(codes),
                bits_total=8 * m.nbytes / codes.size, n_escapes=int(len(enc["esc_pos"])),
-               t_rans_us=t_rans, t_bf16_us=t_bf16,
+               t_rans_us=t_rans, t_bf16_us=t_bf16, t_bf16_hip_us=t_bf16_hip,
                effective_GBps=rows * cols * 2 / t_rans / 1e3,
                compressed_GBps=m.nbytes / t_rans / 1e3,
                speedup_vs_bf16=t_bf16 / t_rans, rel_l2_vs_f64=err, copies=ncopy)
