@@ -152,12 +152,12 @@ def timeit(fn, iters=200):
 
 def copies_for(iters, nbytes, rotate_bytes=512 << 20):
     """Distinct copies of an nbytes operand for a rotated run of `iters`
-    launches: n = ceil(rotate_bytes / nbytes) copies when iters >= n (the
-    timed launches cycle through them, so every copy is read again only after
-    rotate_bytes of other copies), else iters + n (the timed launches use
-    the first iters copies; an untimed flush replay reads the other n just
-    before them)."""
-    n = max(2, -(-rotate_bytes // nbytes))
+    launches: n = ceil(rotate_bytes / nbytes) + 1 copies when iters >= n
+    (the timed launches cycle through them, so every copy is read again only
+    after the other n - 1, at least rotate_bytes), else iters + n (the timed
+    launches use the first iters copies; an untimed flush replay reads the
+    other n just before them)."""
+    n = max(2, -(-rotate_bytes // nbytes) + 1)
     return n if iters >= n else iters + n
 
 
@@ -611,6 +611,39 @@ def configs():
               flush=True)
 
 
+def comparators(rows=1536, cols=8960, iters=100, rotate_bytes=512 << 20):
+    """The uncompressed and fixed-rate comparators alone on one shape,
+    rotated over >= rotate_bytes of copies: the library's dense bf16_gemv
+    (random bf16 weights) and the int4 GEMV (random nibbles; its time
+    includes the host fold x*step, as Int4Matrix.gemv does).  Prints one
+    JSON line: rans_bench.py comparators [ROWS COLS]."""
+    lib = rans.build()
+    g = torch.Generator(device="cuda").manual_seed(rows + cols)
+    W = torch.randn(rows, cols, device="cuda", generator=g).bfloat16()
+    nW = copies_for(iters, rows * cols * 2, rotate_bytes)
+    mbs = [rans.Bf16Matrix(W, lib)] + [rans.Bf16Matrix(W.clone(), lib) for _ in range(nW - 1)]
+    xb = torch.randn(cols, device="cuda", generator=g).bfloat16()
+    yb = torch.empty(rows, device="cuda")
+    t_bf16 = timeit_graph([lambda mb=mb: mb.gemv(xb, yb) for mb in mbs], iters)
+    del mbs, W
+    codes = np.random.default_rng(rows + cols).integers(-8, 8, size=(rows, cols), dtype=np.int32)
+    step = torch.rand(cols) + 0.5
+    m4 = rans.Int4Matrix(codes, step, lib)
+    n4 = copies_for(iters, rows * cols // 2, rotate_bytes)
+    m4s = [m4] + [m4.clone() for _ in range(n4 - 1)]
+    x = torch.randn(cols, device="cuda")
+    y4 = torch.empty(rows, device="cuda")
+    t_int4 = timeit_graph([lambda mm=mm: mm.gemv(x, y4) for mm in m4s], iters)
+    del m4s, m4
+    torch.cuda.empty_cache()
+    r = dict(rows=rows, cols=cols, t_bf16_hip_us=t_bf16, bf16_GBps=rows * cols * 2 / t_bf16 / 1e3,
+             bf16_copies=nW, t_int4_us=t_int4, int4_GBps=rows * cols / 2 / t_int4 / 1e3,
+             int4_copies=n4)
+    print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}),
+          flush=True)
+    return r
+
+
 def profile(rows=25600, cols=5120, bits=2.25, dist="student3", escape_frac=0.01, R=0, C=0,
             launches=20, fetch="refill"):
     """One encoded matrix launched `launches` times at batch 1, then at
@@ -635,7 +668,9 @@ def profile(rows=25600, cols=5120, bits=2.25, dist="student3", escape_frac=0.01,
 
 
 if __name__ == "__main__":
-    if sys.argv[1] == "profile":
+    if sys.argv[1] == "comparators":
+        comparators(*(int(v) for v in sys.argv[2:4]))
+    elif sys.argv[1] == "profile":
         types = (int, int, float, str, float, int, int, int, str)
         profile(*(t(v) for t, v in zip(types, sys.argv[2:])))
     elif sys.argv[1] == "chain":  # chain [grouped|separate|both] [layers] [batch]
