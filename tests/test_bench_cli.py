@@ -28,3 +28,22 @@ def test_no_gpu_is_refused():
     assert r.returncode == 2
     assert "needs a ROCm GPU" in r.stderr
     assert r.stdout.strip() == ""
+
+
+@pytest.mark.parametrize("nbytes", [1 << 20, 6_256_120, 27_525_120, 47_185_920, 178_257_920,
+                                    356_515_840, 600 << 20])
+@pytest.mark.parametrize("iters", [1, 20, 100, 200])
+def test_rotation_covers_the_caches(nbytes, iters):
+    """copies_for's rotation: when the timed launches cycle through the
+    copies, every copy is read again only after at least 512 MiB of the
+    others; when they use fewer copies than that, the untimed flush reads at
+    least 512 MiB of the rest just before them."""
+    sys.path.insert(0, os.path.join(ROOT, "vram-compression_amd"))
+    import rans_bench as B
+    rot = 512 << 20
+    n = B.copies_for(iters, nbytes, rot)
+    assert n >= 2
+    if iters >= n:
+        assert (n - 1) * nbytes >= rot
+    else:
+        assert (n - iters) * nbytes >= rot
