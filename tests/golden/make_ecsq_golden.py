@@ -5,9 +5,11 @@ beside the reference's published ones.
     python tests/golden/make_ecsq_golden.py          # writes ecsq_wf_kv.npz, ecsq_wf_stats.json
 
 Run in the build container only (CPU, torch; about a minute).  The
-quantiser is restated from the documented steps of exp/quant.py (it is not
-imported): hinv_chol (quant.py:28-45), gptq (quant.py:48-72) and ecsq with
-waterfilling (quant.py:116-156).  Its inputs are synthetic, since the
+quantiser is the reference's own: exp/quant.py is imported from the
+reference checkout ($REFERENCE, default /root/reference) and its
+ecsq(W, H, 3.25, waterfill=True) (quant.py:122-156) quantises each group;
+the codes and per-column steps of its final GPTQ pass are recorded from its
+_ecsq_run (quant.py:117-119).  The layers are synthetic, since the
 reference's model and calibration text need network access:
 
 - weights: N(0, 0.02^2) scaled per input column by a log-normal factor, so
@@ -28,6 +30,7 @@ Outputs (both committed):
   outside [-127, 127]) and the largest |code|, beside the published layer 0
   levels and the published range over the 28 layers
   (results/Qwen2.5-1.5B__ecsq_wf_3.25.json)."""
+import importlib.util
 import json
 import math
 import os
@@ -38,8 +41,8 @@ import numpy as np
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-REF_RESULTS = "/root/reference/results/Qwen2.5-1.5B__ecsq_wf_3.25.json"
-GROUP = 128
+REF = os.environ.get("REFERENCE", "/root/reference")
+REF_RESULTS = os.path.join(REF, "results", "Qwen2.5-1.5B__ecsq_wf_3.25.json")
 BITS = 3.25
 
 # group: rows, cols, kurtosis target, diag(H) max/median target
@@ -47,91 +50,40 @@ GROUPS = {"qkv": (2048, 1536, 1.10, 1609.0), "o": (1536, 1536, 0.97, 177.5),
           "gate_up": (17920, 1536, 0.18, 294.0), "down": (1536, 8960, 0.32, 1758.4)}
 
 
-def entropy_bits(codes):
-    """Zero-order entropy of the integer codes (quant.py:22-25), by counts."""
-    c = codes.reshape(-1).long()
-    counts = torch.bincount(c - c.min())
-    p = counts[counts > 0].double() / c.numel()
-    return float(-(p * p.log2()).sum())
+def load_quant():
+    """The reference's quantiser module, exp/quant.py, imported from the
+    reference checkout (it needs only math and torch)."""
+    spec = importlib.util.spec_from_file_location("quant", os.path.join(REF, "exp", "quant.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["quant"] = mod
+    spec.loader.exec_module(mod)
+    return mod
 
 
-def hinv_chol(H, percdamp=0.01):
-    """Upper Cholesky factor of (H + damp*I)^-1 in float64 (quant.py:28-45):
-    dead channels get a unit diagonal, damp = percdamp * mean diag, raised
-    again while the factorisation fails."""
-    H = H.double().clone()
-    dead = torch.diag(H) == 0
-    H[dead, dead] = 1
-    damp = percdamp * torch.diag(H).mean()
-    H.diagonal().add_(damp)
-    while True:
-        L, info = torch.linalg.cholesky_ex(H)
-        if info == 0:
-            break
-        H.diagonal().add_(damp)
-    Hinv = torch.cholesky_inverse(L)
-    U = torch.linalg.cholesky(Hinv, upper=True)
-    return U.float(), dead
+def ecsq_wf(quant, W, H, target_bits):
+    """Runs the reference's quant.ecsq(W, H, target_bits, waterfill=True)
+    (exp/quant.py:122-156) and returns its integer codes and per-column
+    steps with its info dict.  ecsq returns only the dequantised weights, so
+    its module-level GPTQ pass _ecsq_run (exp/quant.py:117-119), which it
+    calls last with the final steps, is wrapped to record those steps and
+    the codes of that call."""
+    seen = {}
+    run = quant._ecsq_run
 
+    def record(W_, Hinv, steps):
+        Q, C = run(W_, Hinv, steps)
+        seen["steps"], seen["codes"] = steps.clone(), C.clone()
+        return Q, C
 
-def gptq(W, Hinv, steps, blocksize=GROUP):
-    """GPTQ / LDLQ with error feedback (quant.py:48-72) for the ECSQ column
-    quantiser of quant.py:117-119: code = round(w / step_i), value = code *
-    step_i.  Within a block each column's error, scaled by the inverse
-    factor's diagonal, is pushed onto the block's later columns; at the end
-    of a block its errors are pushed onto all later columns."""
-    W = W.clone()
-    n = W.shape[1]
-    C = torch.zeros(W.shape, dtype=torch.int32)
-    for i1 in range(0, n, blocksize):
-        i2 = min(i1 + blocksize, n)
-        W1 = W[:, i1:i2].clone()
-        E1 = torch.zeros_like(W1)
-        Hi = Hinv[i1:i2, i1:i2]
-        for i in range(i2 - i1):
-            w = W1[:, i]
-            c = torch.round(w / steps[i1 + i])
-            q = c * steps[i1 + i]
-            C[:, i1 + i] = c.int()
-            err = (w - q) / Hi[i, i]
-            W1[:, i:] -= err.unsqueeze(1) @ Hi[i, i:].unsqueeze(0)
-            E1[:, i] = err
-        W[:, i2:] -= E1 @ Hinv[i1:i2, i2:]
-    return C
-
-
-def ecsq_wf(W, H, target_bits):
-    """ECSQ with waterfilling (quant.py:122-156): per-column steps c * d_i with
-    d = diag of the upper Cholesky factor of H^-1 over its mean; 16 bits of
-    side information per column; c from 40 bisection steps on the
-    round-to-nearest entropy, then two secant corrections on the GPTQ codes
-    (dH/dlog2 c ~ -1), then the final GPTQ pass.  Returns codes, steps, info."""
-    Hinv, dead = hinv_chol(H)
-    W = W.clone()
-    W[:, dead] = 0
-    d = torch.diag(Hinv)
-    base = d / d.mean()
-    side = 16 * W.shape[1] / W.numel()
-    target = target_bits - side
-
-    def rtn_H(logc):
-        return entropy_bits(torch.round(W / (math.exp(logc) * base)))
-
-    lo, hi = math.log(W.std().item()) - 12, math.log(W.std().item()) + 4
-    for _ in range(40):
-        mid = (lo + hi) / 2
-        if rtn_H(mid) > target:
-            lo = mid
-        else:
-            hi = mid
-    logc = (lo + hi) / 2
-    for _ in range(2):
-        C = gptq(W, Hinv, math.exp(logc) * base)
-        logc += (entropy_bits(C) - target) * math.log(2)
-    steps = math.exp(logc) * base
-    C = gptq(W, Hinv, steps)
-    h = entropy_bits(C)
-    return C, steps, dict(bpw=h + side, code_entropy=h, levels=int(torch.unique(C).numel()))
+    quant._ecsq_run = record
+    try:
+        Q, info = quant.ecsq(W, H, target_bits, True)
+    finally:
+        quant._ecsq_run = run
+    C, steps = seen["codes"], seen["steps"]
+    # the recorded pass is the one whose output ecsq returned
+    assert torch.equal(C.float() * steps, Q)
+    return C, steps, info
 
 
 def synth_layer(rows, cols, kurt, diag_ratio, gen, m=4096, rank=32):
@@ -157,14 +109,15 @@ def synth_layer(rows, cols, kurt, diag_ratio, gen, m=4096, rank=32):
 def main():
     torch.set_num_threads(min(8, os.cpu_count() or 1))
     gen = torch.Generator().manual_seed(1536)
+    quant = load_quant()
     ref = json.load(open(REF_RESULTS))["infos"]
-    out = {"bits": BITS, "method": "ecsq_wf (restated), synthetic random-init layer", "groups": {}}
+    out = {"bits": BITS, "method": "ecsq_wf (exp/quant.py ecsq, imported), synthetic random-init layer", "groups": {}}
     fixture = None
     for g, (rows, cols, kurt, ratio) in GROUPS.items():
         t0 = time.time()
         W, H = synth_layer(rows, cols, kurt, ratio, gen)
         dh = torch.diag(H)
-        C, steps, info = ecsq_wf(W, H, BITS)
+        C, steps, info = ecsq_wf(quant, W, H, BITS)
         c = C.numpy()
         pub = [x for x in ref if x["group"] == g]
         pub0 = [x for x in pub if x["layer"] == 0][0]

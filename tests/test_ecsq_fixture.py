@@ -1,6 +1,7 @@
 """Codes with ECSQ-GPTQ + waterfilling statistics (tests/golden/ecsq_wf_kv.npz,
-written by tests/golden/make_ecsq_golden.py from a restatement of
-exp/quant.py:116-156 on a synthetic random-init layer): the fixture agrees
+written by tests/golden/make_ecsq_golden.py, which imports the reference's
+exp/quant.py and runs its ecsq with waterfilling, quant.py:122-156, on a
+synthetic random-init layer): the fixture agrees
 with its recorded statistics, those sit inside the reference's published
 range (results/Qwen2.5-1.5B__ecsq_wf_3.25.json, copied into the statistics
 file by the generator), and the codes, escapes included, survive the w64

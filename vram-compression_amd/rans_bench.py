@@ -116,9 +116,9 @@ ECSQ_FIXTURE = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__fi
 def ecsq_fixture(rows=None):
     """Codes with ECSQ-GPTQ + waterfilling statistics and their per-column
     steps: the k projection (256 x 1536) of a synthetic random-init
-    Qwen2.5-1.5B layer quantised at 3.25 b/w by a restatement of the
-    reference's ecsq_wf method (exp/quant.py:116-156; written by
-    tests/golden/make_ecsq_golden.py).  rows: a multiple of 256, the 256 rows
+    Qwen2.5-1.5B layer quantised at 3.25 b/w by the reference's own ecsq
+    with waterfilling (exp/quant.py:122-156, imported by
+    tests/golden/make_ecsq_golden.py, which wrote the fixture).  rows: a multiple of 256, the 256 rows
     repeated to that height.  Returns (int32 codes, float32 steps)."""
     z = np.load(ECSQ_FIXTURE)
     codes = z["codes"].astype(np.int32)
