@@ -306,3 +306,27 @@ def test_r20_round_trip(rans, oracle):
     assert rans.tiling_of(enc) == (20, 640, 1)
     np.testing.assert_array_equal(rans.decode_ref(enc), codes)
     np.testing.assert_array_equal(oracle.w64_decode(enc), codes)
+
+
+def test_layout_tags_keep_the_two_formats_apart(rans, oracle):
+    """encode() writes the w64 layout and says so; the reference-layout
+    encoder says ref32; an untagged dict is w64 when it carries tile
+    offsets (the reference's own encode writes none).  Each matrix class
+    refuses the other layout before it needs a GPU, so a w64 dict cannot
+    be decoded as 32-lane streams by the reference's entry points."""
+    codes = oracle.synth_codes(64, 256, 3.0, seed=5)
+    w64 = rans.encode(codes, 8, 256)
+    ref = rans.encode_reference_layout(codes, 8, 256)
+    assert w64["layout"] == rans.LAYOUT_W64 and ref["layout"] == rans.LAYOUT_REF32
+    assert rans.layout_of({k: v for k, v in w64.items() if k != "layout"}) == rans.LAYOUT_W64
+    untagged = {k: v for k, v in ref.items() if k != "layout"}
+    assert rans.layout_of(untagged) == rans.LAYOUT_REF32
+    step = np.ones(256, np.float32)
+    with pytest.raises(AssertionError, match="32-lane"):
+        rans.ReferenceLayoutMatrix(w64, step, None)
+    with pytest.raises(AssertionError, match="w64"):
+        rans.RansMatrix(ref, step, None)
+    with pytest.raises(AssertionError, match="w64"):
+        rans.RansMatrix(untagged, step, None)
+    with pytest.raises(AssertionError, match="unknown"):
+        rans.layout_of(dict(w64, layout="w32"))

@@ -91,3 +91,47 @@ def test_save_rejects_inconsistent_entries(rans, tmp_path, entries):
     e["step"] = e["step"][:-1]  # one column short
     with pytest.raises(AssertionError):
         rans_io.save(str(tmp_path / "x.w64"), [e])
+
+
+def test_version_5_written_and_4_read(rans, tmp_path, entries):
+    """The writer stamps version 5; a version-4 file (the same layout, the
+    appended-columns slot zero) still loads; other versions are refused."""
+    import rans_io
+    path = str(tmp_path / "set.w64")
+    rans_io.save(path, entries)
+    raw = bytearray(open(path, "rb").read())
+    assert int.from_bytes(raw[8:12], "little") == rans_io.VERSION == 5
+    for version, ok in ((4, True), (3, False), (6, False)):
+        p = str(tmp_path / f"v{version}.w64")
+        raw[8:12] = version.to_bytes(4, "little")
+        open(p, "wb").write(raw)
+        if ok:
+            got = rans_io.load(p)
+            for e, g in zip(entries, got):
+                np.testing.assert_array_equal(rans.decode_ref(g["enc"]), e["codes"])
+        else:
+            with pytest.raises(ValueError, match="version"):
+                rans_io.load(p)
+
+
+def test_appended_columns_round_trip(rans, oracle, tmp_path):
+    """A matrix whose cols is an odd multiple of 32 (stored with 32 appended
+    columns) keeps its own shape, step and codes through a version-5 file,
+    next to one without appended columns."""
+    import rans_io
+    odd = oracle.synth_codes(64, 224, 3.0, seed=11)
+    even = oracle.synth_codes(64, 256, 3.0, seed=12)
+    ents = []
+    for name, codes in (("odd", odd), ("even", even)):
+        enc = rans.encode(codes, 8, 32 if codes.shape[1] % 64 else 64)
+        step = np.linspace(0.5, 1.5, codes.shape[1]).astype(np.float32)
+        ents.append(dict(name=name, enc=enc, step=step, codes=codes))
+    path = str(tmp_path / "odd.w64")
+    rans_io.save(path, ents)
+    got = rans_io.load(path)
+    assert rans.stream_cols(got[0]["enc"]) == 256 and rans.stream_cols(got[1]["enc"]) == 256
+    for e, g in zip(ents, got):
+        assert tuple(g["enc"]["shape"]) == e["codes"].shape
+        assert g["enc"]["layout"] == rans.LAYOUT_W64
+        np.testing.assert_array_equal(g["step"], e["step"])
+        np.testing.assert_array_equal(rans.decode_ref(g["enc"]), e["codes"])

@@ -37,6 +37,10 @@ ESC = 0  # escape symbol: codes outside [-127, 127]
 LANES = 64
 
 X_F32, X_BF16 = 0, 1
+# stream layouts, recorded as enc["layout"]: the wavefront-interleaved w64
+# format of `encode`, and the reference's own 32-lane format
+# (encode_reference_layout, or the reference's encode itself)
+LAYOUT_W64, LAYOUT_REF32 = "w64", "ref32"
 # rans_w64_matrix.flags: word fetch of the GEMV (0 = library default), and
 # the empty-side-table promise (set by RansMatrix itself)
 F_WORDS_ALWAYS, F_WORDS_REFILL, F_WORDS_MASK, F_NO_ESCAPES = 1, 2, 3, 4
@@ -302,7 +306,11 @@ def encode(codes, R, C, S=None, threads=None):
     shape, bits_payload, bits_state_offs, bits_table, entropy_model,
     rans.py:93-98) and the w64 stream: tile_off, slen, states, the escape
     side table (esc_tileptr, esc_pos, esc_val), tile_R, tile_C, S,
-    stream_cols, max_tile_words, max_state_words, bits_escape.  shape is
+    stream_cols, max_tile_words, max_state_words, bits_escape, and
+    layout = "w64".  offs keeps the reference's meaning (each stream's first
+    word) but there is one stream per 64-lane state, not per 32-lane lane:
+    the dict cannot go to launch_rans_gemv / launch_rans_decode or to
+    ReferenceLayoutMatrix, which refuses it.  shape is
     the matrix's own; the stream holds stream_cols = w64_stream_cols(cols)
     columns (32 columns of code 0 appended when cols % 64 == 32).  Bit
     accounting, per weight of the matrix: bits_payload (renormalisation
@@ -362,9 +370,20 @@ def encode(codes, R, C, S=None, threads=None):
                bits_state_offs=(40 * nstates + 32 * (ntiles + 1) + 16 * pad_words) / N,
                bits_table=32 * M / N,
                bits_escape=(32 * (ntiles + 1) + 32 * nesc) / N,
-               entropy_model=entropy_model)
+               entropy_model=entropy_model, layout=LAYOUT_W64)
     enc["offs"] = stream_offsets(enc)
     return enc
+
+
+def layout_of(enc):
+    """The stream layout of an encoded dict: its "layout" tag, or for an
+    untagged dict (the reference's own encode writes none) "w64" when it
+    carries the w64 tile offsets and "ref32" otherwise."""
+    tag = enc.get("layout")
+    if tag is None:
+        return LAYOUT_W64 if "tile_off" in enc else LAYOUT_REF32
+    assert tag in (LAYOUT_W64, LAYOUT_REF32), f"unknown stream layout {tag!r}"
+    return tag
 
 
 def tiling_of(enc):
@@ -520,6 +539,9 @@ class RansMatrix:
         here when the matrix has no escapes.  The 4-byte table image is
         uploaded only where the library would use it (rans_gemv_table4 at
         batch 1, bf16 x) or F_TABLE4 asks for it."""
+        assert layout_of(enc) == LAYOUT_W64, \
+            "RansMatrix takes the w64 layout of encode(); the reference's 32-lane layout " \
+            "runs on ReferenceLayoutMatrix"
         _require_gpu()
         if lib is None:
             raise RuntimeError("librans_hip.so not loaded")
@@ -750,8 +772,8 @@ def encode_reference_layout(codes, R, C, threads=None):
     """The reference's encode (kernel/rans.py:62-98) on its own 32-lane
     layout: words, offs and table as it writes them, in its dict (words,
     offs, table, R, C, shape, bits_payload, bits_state_offs, bits_table,
-    entropy_model).  The input of ReferenceLayoutMatrix and of the
-    reference-format entry points; `encode` gives the w64 layout, which
+    entropy_model) plus layout = "ref32".  The input of
+    ReferenceLayoutMatrix and of the reference-format entry points; `encode` gives the w64 layout, which
     decodes far faster.  codes must lie in [-128, 127]."""
     codes = np.ascontiguousarray(codes, dtype=np.int32)
     assert codes.ndim == 2 and codes.size > 0, "codes must be a non-empty matrix"
@@ -777,7 +799,8 @@ def encode_reference_layout(codes, R, C, threads=None):
     return dict(words=buf[:int(info[0])].copy(), offs=offs, table=table, R=R, C=C,
                 shape=codes.shape, bits_payload=16 * int(info[1]) / n,
                 bits_state_offs=64 * lanes / n, bits_table=32 * M / n,
-                entropy_model=float(-(cnt[used] * np.log2(fr[used] / M)).sum() / n))
+                entropy_model=float(-(cnt[used] * np.log2(fr[used] / M)).sum() / n),
+                layout=LAYOUT_REF32)
 
 
 class ReferenceLayoutMatrix:
@@ -789,6 +812,10 @@ class ReferenceLayoutMatrix:
     the w64 layout is the fast path."""
 
     def __init__(self, enc, step, lib):
+        assert layout_of(enc) == LAYOUT_REF32, \
+            "ReferenceLayoutMatrix takes the reference's 32-lane layout " \
+            "(encode_reference_layout, or the reference's encode); the w64 dict of encode() " \
+            "has one offs entry per 64-lane state and runs on RansMatrix"
         _require_gpu()
         self.lib = lib
         self.R, self.C = int(enc["R"]), int(enc["C"])

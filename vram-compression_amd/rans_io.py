@@ -9,9 +9,12 @@ Layout (all integers little endian, every section 64-byte aligned):
 
     header, 64 bytes
         magic      8 bytes  b"VRAMCW64"
-        version    u32      4 (1 to 3 held a row-CSR side table, 16-bit
-                            stream offsets or a 32-bit side table; they are
-                            not read)
+        version    u32      5 (written); 4 is also read: the same layout,
+                            whose record slot for the appended columns was
+                            zero padding in its first files, so they read
+                            as 0 appended columns (1 to 3 held a row-CSR
+                            side table, 16-bit stream offsets or a 32-bit
+                            side table; they are not read)
         nmat       u32      number of matrices
         index_off  u64      byte offset of the index
         file_bytes u64      total file size (truncation check)
@@ -27,6 +30,7 @@ Layout (all integers little endian, every section 64-byte aligned):
                    esc_pos, esc_val, step                             u64 x 9
         crc32 of the nine sections, in that order                     u32
         appended columns (0, or 32 when the matrix's cols % 64 == 32)  i32
+                   (new in version 5; version 4 files hold 0 here)
         zero padding to 256 bytes
     sections
         words u16[nwords], tile_off u32[ntiles+1], slen u8[nstates],
@@ -47,7 +51,8 @@ import numpy as np
 import rans
 
 MAGIC = b"VRAMCW64"
-VERSION = 4
+VERSION = 5
+READ_VERSIONS = (4, 5)
 _HEADER = struct.Struct("<8sIIQQ32x")
 _RECORD = struct.Struct("<64s8i5Qd9QIi")
 RECORD_BYTES = 256
@@ -134,7 +139,7 @@ def load(path, verify=True, mmap=True):
         magic, version, nmat, index_off, file_bytes = _HEADER.unpack(head)
         if magic != MAGIC:
             raise ValueError("not a w64 container: bad magic")
-        if version != VERSION:
+        if version not in READ_VERSIONS:
             raise ValueError(f"unsupported w64 container version {version}")
         if file_bytes != size:
             raise ValueError(f"truncated or padded file: header says {file_bytes} bytes, "
@@ -183,7 +188,7 @@ def load(path, verify=True, mmap=True):
                    bits_state_offs=(40 * nstates + 32 * (ntiles + 1) + 16 * pad) / N,
                    bits_table=32 * rans.M / N,
                    bits_escape=(32 * (ntiles + 1) + 32 * nesc) / N,
-                   entropy_model=entropy_model)
+                   entropy_model=entropy_model, layout=rans.LAYOUT_W64)
         enc["offs"] = rans.stream_offsets(enc)
         out.append(dict(name=name, enc=enc, step=arrays["step"], flags=flags))
     return out
