@@ -161,3 +161,24 @@ def test_header_compiles_as_c(tmp_path):
     for std, lang in (("c99", "c"), ("c++17", "c++")):
         subprocess.check_call([gcc, f"-std={std}", "-x", lang, "-fsyntax-only", f"-I{inc}",
                                "-I/opt/rocm/include", "-D__HIP_PLATFORM_AMD__", str(src)])
+
+
+def test_fused_rows_limit_follows_the_planner(rans, lib):
+    """The crossover to decode + dense GEMM is 16 rows only where the
+    library runs 5-8 rows as one batch-8 launch: a single matrix with one
+    state per lane, tiles of at most 8 rows and no split over column
+    groups.  Split-K tilings, taller tiles, more states per lane and
+    grouped launches run batch-4 launches and cross over at 8."""
+    single = _desc(rans, cols=2048)            # 8 column tiles: one workgroup per tile row
+    assert lib.rans_gemv_workspace_bytes(ctypes.byref(single), 8) == 0
+    assert rans.fused_rows_limit(single, lib) == 16
+    assert rans.fused_rows_limit(single, lib, grouped=True) == 8
+    split = _desc(rans)                         # 16 column tiles: two column groups
+    assert lib.rans_gemv_workspace_bytes(ctypes.byref(split), 8) > 0
+    assert rans.fused_rows_limit(split, lib) == 8
+    tall = _desc(rans, rows=256, cols=2048, R=16)
+    assert rans.fused_rows_limit(tall, lib) == 8
+    two = _desc(rans, cols=2048, C=256, S=2)
+    assert rans.fused_rows_limit(two, lib) == 8
+    bad = _desc(rans, mtw=70000)                # outside the format: no launch at all
+    assert rans.fused_rows_limit(bad, lib) == 8

@@ -523,6 +523,22 @@ def decode_ref(enc):
     return out[:, :cols].astype(np.int64)
 
 
+def fused_rows_limit(desc, lib, grouped=False):
+    """Rows of x up to which the fused GEMV beats decoding to bf16 and a
+    dense GEMM on MI355X: 16 where a batch of 5 to 8 rows runs as one launch
+    of the batch-8 kernel (1536x8960 at 16 rows 29.9 against 38.6 us,
+    1536x1536 14.1 against 14.6), else 8 (batch-4 launches: 8960x1536 at 12
+    rows 32.7 against 25.6 us, 25600x5120 158.6 against 150.4).  The
+    library's planner takes the batch-8 kernel only for a single matrix with
+    one state per lane, tiles of at most 8 rows and one workgroup per tile
+    row (no split-K: rans_gemv_workspace_bytes is 0); grouped launches
+    (grouped=True) have no batch-8 kernel.  desc: a RansMatrixDesc; lib:
+    the loaded library (the query is host code, no GPU needed)."""
+    batch8 = (not grouped and desc.S == 1 and desc.R <= 8 and
+              lib.rans_gemv_workspace_bytes(ctypes.byref(desc), 8) == 0)
+    return 16 if batch8 else 8
+
+
 # ------------------------------------------------------------------- device
 def _require_gpu():
     if not torch.cuda.is_available():
@@ -605,13 +621,9 @@ class RansMatrix:
 
     @property
     def fused_rows_limit(self):
-        """Rows of x up to which the fused GEMV beats decoding to bf16 and a
-        dense GEMM on MI355X: 16 where the batch-8 kernel exists (one state
-        per lane, tiles of at most 8 rows: 1536x8960 at 16 rows 29.9 against
-        38.6 us, 1536x1536 14.1 against 14.6), else 8 (the batch-4 kernel:
-        8960x1536 at 12 rows 32.7 against 25.6 us, 25600x5120 158.6 against
-        150.4)."""
-        return 16 if self._desc.S == 1 and self._desc.R <= 8 else 8
+        """Rows of x up to which this matrix's own GEMV launch beats
+        decoding to bf16 and a dense GEMM (module-level fused_rows_limit)."""
+        return fused_rows_limit(self._desc, self.lib)
 
     def tune(self, batch=1, x_dtype=torch.bfloat16, iters=20):
         """Time the two word-fetch policies of the GEMV on this matrix and

@@ -26,9 +26,10 @@ import rans
 
 # Batches above a matrix's fused_rows_limit decode the weight to bf16 and
 # use the dense GEMM.  The fused GEMV runs up to 8 vectors per launch (4
-# where tiles are taller than 8 rows), so its time grows with the batch
+# where tiles are taller than 8 rows, the launch splits over column groups,
+# or matrices share a grouped launch), so its time grows with the batch
 # while decode+GEMM stays flat: on MI355X the fused path wins up to 16 rows
-# with the batch-8 kernel and up to 8 without it (RansMatrix.fused_rows_limit).
+# with the batch-8 kernel and up to 8 without it (rans.fused_rows_limit).
 
 
 def _entropy(codes):
@@ -82,7 +83,8 @@ class LinearGroup:
         if (self._x is not None and self._x() is x and self._version == x._version
                 and i in self._pending):
             return self._pending.pop(i)
-        if xd.shape[0] > self.members[0].matrix.fused_rows_limit:
+        m0 = self.members[0].matrix
+        if xd.shape[0] > rans.fused_rows_limit(m0._desc, m0.lib, grouped=True):
             # all members decoded into row slices of one bf16 weight, one GEMM
             w = torch.empty(sum(m.out_features for m in self.members), xd.shape[1],
                             device="cuda", dtype=torch.bfloat16)
