@@ -71,3 +71,48 @@ def test_noalloc_matches_workspace_launch(rans, oracle, lib):
                                   step.astype(np.float64))
             err = float(np.linalg.norm(y.cpu().numpy() - ref) / np.linalg.norm(ref))
             assert err <= REL_L2, err
+
+
+@pytest.mark.gpu
+def test_noalloc_under_graph_capture(rans, lib):
+    """The entry point that allocates nothing is meant for callers under
+    HIP graph capture.  Split-K launches at batch 1 and 4 are captured in
+    one graph and replayed four times, with eager launches of the same
+    entry point and synchronisations between replays: every replay equals
+    the eager workspace launch bit for bit, so the scratch counters return
+    to zero under replay as well as eagerly."""
+    if not torch.cuda.is_available():
+        raise RuntimeError("GPU tests need a ROCm device")
+    import rans_bench as B
+    rows, cols, R, C = 768, 8192, 8, 512  # 16 column tiles: two column groups
+    print(f"case noalloc graph {rows}x{cols} R={R} C={C}", flush=True)
+    codes = B.synth_codes_full(rows, cols, 3.25, seed=7, escape_frac=0.002)
+    step = B.lognormal_steps(cols, seed=7)
+    m = rans.RansMatrix(rans.encode(codes, R, C, 1), torch.from_numpy(step), lib)
+    assert lib.rans_gemv_workspace_bytes(ctypes.byref(m._desc), 1) > 0
+    xs = {b: torch.randn(b, cols, device="cuda").bfloat16() for b in (1, 4)}
+    want = {b: m.gemv(x) for b, x in xs.items()}
+    ys = {b: torch.empty(b, rows, device="cuda") for b in xs}
+    torch.cuda.synchronize()
+
+    def call(b, y, stream):
+        return lib.rans_w64_gemv_noalloc(ctypes.byref(m._desc), xs[b].data_ptr(), rans.X_BF16,
+                                         b, y.data_ptr(), stream)
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s = torch.cuda.current_stream().cuda_stream
+        rcs = [call(b, ys[b], s) for b in (1, 4)]
+    assert rcs == [0, 0], rcs
+    other = torch.empty(4, rows, device="cuda")
+    for rep in range(4):
+        for y in ys.values():
+            y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for b in xs:
+            assert torch.equal(ys[b], want[b]), (rep, b)
+        # eager work on the same scratch between replays
+        assert call(4, other, torch.cuda.current_stream().cuda_stream) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(other, want[4]), rep
