@@ -22,6 +22,7 @@ Prints one JSON line.  `value` is the bf16-equivalent effective weight
 throughput rows*cols*2 bytes / time per GEMV.
 """
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -49,9 +50,39 @@ DEFAULT_TILING = (3, 2240, 1)
 # passes (FETCH_SIZE, then WRITE_SIZE) over 50 rotated launches.  Each counter
 # is scaled by what it reads for an elementwise kernel that reads and writes
 # 256 MiB: reads x2.0, writes x1.0.  Commands and counts:
-# profiles/rans_w64_gemv_1536x8960_3.25b.md.  Keyed by (R, C, S, word fetch).
-PMC_TRAFFIC_KIB = {(3, 2240, 1, "refill"): (3445.6, 12.0)}
+# profiles/rans_w64_gemv_1536x8960_3.25b.md.  Keyed by (R, C, S, word fetch)
+# and by the hash of the library sources they were measured on
+# (library_source_hash): with other sources the line reports traffic null.
+PMC_TRAFFIC_KIB = {(3, 2240, 1, "refill"): dict(source_hash="2ab2e23b36a1",
+                                                fetch_kib=3445.6, write_kib=12.0)}
 PMC_FETCH_FACTOR, PMC_WRITE_FACTOR = 2.0, 1.0
+
+
+def library_source_hash():
+    """First 12 hex digits of the SHA-256 of the library's sources and
+    header (rans.SOURCES, rans.HEADERS, in that order): names the build a
+    counter figure belongs to."""
+    h = hashlib.sha256()
+    for path in rans.SOURCES + rans.HEADERS:
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:12]
+
+
+def pmc_traffic(R, C, S, word_fetch, src_hash):
+    """(HBM bytes per launch, note) of the headline kernel for this tiling
+    and word fetch from the rocprofv3 counters, or (None, why) when no
+    counter figure exists or it was measured on other library sources."""
+    pmc = PMC_TRAFFIC_KIB.get((R, C, S, word_fetch))
+    if pmc is None:
+        return None, "no counter figure for this tiling"
+    if pmc["source_hash"] != src_hash:
+        return None, (f"the counter figure was measured on library sources {pmc['source_hash']}, "
+                      f"these are {src_hash}")
+    t = int((pmc["fetch_kib"] * PMC_FETCH_FACTOR + pmc["write_kib"] * PMC_WRITE_FACTOR) * 1024)
+    return t, ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, scaled x2.0 / x1.0, "
+               f"measured on library sources {src_hash} "
+               "(profiles/rans_w64_gemv_1536x8960_3.25b.md)")
 
 
 def algorithmic_bytes(enc, rows, cols, batch=1):
@@ -242,6 +273,9 @@ def main():
     ap.add_argument("--no-rocblas", action="store_true")
     ap.add_argument("--no-chain", action="store_true",
                     help="skip the per-token chain (196 GEMVs, grouped launches)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other benchmark configurations (q_proj at 4.25 bits, the MLP "
+                         "shapes at 2.25 bits with escapes, the 27B-class shapes at batch 1 and 4)")
     ap.add_argument("--no-ecsq", action="store_true",
                     help="skip the row with ECSQ-GPTQ + waterfilling code statistics")
     ap.add_argument("--no-reflayout", action="store_true",
@@ -368,11 +402,17 @@ def main():
         rocblas["int4_us_per_gemv"] = graph_time_us([lambda m4=m4: m4.gemv(xf, y4) for m4 in m4s],
                                                     args.steps, args.warmup, rotate=n4)
         del m4s, m4
-        m = rans.RansMatrix(enc, step_t, lib)
+        # decode to bf16, then F.linear (the reference's t_decode_then_cublas),
+        # over the rotated compressed copies like every other comparator; the
+        # bf16 buffer is the decode's output, rewritten by every call
+        ndc = copies_for(args.steps, comp)
+        mds = [rans.RansMatrix(enc, step_t, lib) for _ in range(ndc)]
         buf = torch.empty(ROWS, COLS, device="cuda", dtype=torch.bfloat16)
         rocblas["decode_then_bf16_us_per_gemv"] = graph_time_us(
-            [lambda: torch.nn.functional.linear(xb, m.decode(buf))], 50, args.warmup)
-        del m, buf
+            [lambda md=md: torch.nn.functional.linear(xb, md.decode(buf)) for md in mds],
+            args.steps, args.warmup, rotate=ndc)
+        rocblas["decode_then_bf16_copies"] = ndc
+        del mds, buf
         torch.cuda.empty_cache()
         print(f"bf16 F.linear: {tb_rot:.2f} us rotated, {tb_hot:.2f} us hot; "
               f"bf16 HIP GEMV: {th_rot:.2f} us rotated", file=sys.stderr, flush=True)
@@ -426,18 +466,61 @@ def main():
         r = B.config_matrix(2048, 1536, 3.25, "ecsq_wf", 0.0, 1, 0, lib, codes=codes_e,
                             step=step_e, iters=args.steps)
         ecsq = {k: r[k] for k in ("rows", "cols", "R", "C", "entropy", "bits_total", "n_escapes",
-                                  "t_rans_us", "t_bf16_us", "effective_GBps", "speedup_vs_bf16",
-                                  "rel_l2_vs_f64", "copies")}
+                                  "t_rans_us", "t_bf16_us", "t_bf16_hip_us", "effective_GBps",
+                                  "speedup_vs_bf16", "speedup_vs_bf16_hip", "algorithmic_bytes",
+                                  "roofline_frac", "rel_l2_vs_f64", "copies")}
         ecsq["workload"] = ("q/k/v-shaped 2048x1536 ECSQ-GPTQ + waterfilling codes at 3.25 b/w "
                             "(246 levels, escapes up to |196|), own per-column steps, bf16 x, "
                             "batch 1")
         torch.cuda.empty_cache()
 
+    # The other configurations of the benchmark, each timed like the
+    # headline (rotated copies, HIP graph), beside F.linear and the library's
+    # bf16_gemv on the same shape and rotation: q_proj 1536x1536 at 4.25 bits,
+    # the MLP shapes at 2.25 bits with 0.1% escapes, and the 27B-class
+    # shapes (Student-t(3) codes at 2.25 bits, 1% escapes, log-normal steps)
+    # at batch 1 and 4.  Both 27B shapes use seed 30720, so the 5120x25600
+    # codes are the 25600x5120 array reshaped (the generator's flat draw does
+    # not depend on the shape): generated once.
+    configs = None
+    if not args.no_configs:
+        configs = []
+        keys = ("rows", "cols", "batch", "R", "C", "S", "word_fetch", "entropy", "bits_total",
+                "n_escapes", "t_rans_us", "t_bf16_us", "t_bf16_hip_us", "effective_GBps",
+                "compressed_GBps", "algorithmic_bytes", "roofline_frac", "speedup_vs_bf16",
+                "speedup_vs_bf16_hip", "rel_l2_vs_f64", "copies", "bf16_copies")
+
+        def add(name, records):
+            for r in (records if isinstance(records, list) else [records]):
+                rec = {"config": name, **{k: r[k] for k in keys}}
+                if r["batch"] > 1:
+                    rec["note"] = ("bf16_gemv takes one vector per launch: t_bf16_hip_us is "
+                                   f"{r['batch']} launches")
+                configs.append(rec)
+                print(f"config {name} B={r['batch']}: {r['t_rans_us']:.2f} us "
+                      f"(F.linear {r['t_bf16_us']:.2f}, bf16_gemv {r['t_bf16_hip_us']:.2f})",
+                      file=sys.stderr, flush=True)
+
+        add("2: q_proj 1536x1536 N(0,1) 4.25 b",
+            B.config_matrix(1536, 1536, 4.25, "gauss", 0.0, 1, 3072, lib, iters=args.steps))
+        add("3: gate/up 8960x1536 Laplace 2.25 b, 0.1% escapes",
+            B.config_matrix(8960, 1536, 2.25, "laplace", 0.001, 1, 10496, lib, iters=args.steps))
+        add("3: down 1536x8960 Laplace 2.25 b, 0.1% escapes",
+            B.config_matrix(1536, 8960, 2.25, "laplace", 0.001, 1, 10496, lib, iters=args.steps))
+        big = B.synth_codes_full(25600, 5120, 2.25, dist="student3", seed=30720,
+                                 escape_frac=0.01)
+        for rows, cols in ((25600, 5120), (5120, 25600)):
+            add(f"5: {rows}x{cols} Student-t(3) 2.25 b, 1% escapes",
+                B.config_matrix(rows, cols, 2.25, "student3", 0.01, (1, 4), 30720, lib,
+                                iters=args.steps, codes=big.reshape(rows, cols),
+                                step=B.lognormal_steps(cols, seed=30720)))
+        del big
+        torch.cuda.empty_cache()
+
     achieved = alg / (t_rot * 1e-6) / 1e9
     fetch_name = {rans.F_WORDS_ALWAYS: "always", rans.F_WORDS_REFILL: "refill"}.get(measure.flags & 3)
-    pmc = PMC_TRAFFIC_KIB.get((R, C, S, fetch_name))
-    traffic = None if pmc is None else \
-        int((pmc[0] * PMC_FETCH_FACTOR + pmc[1] * PMC_WRITE_FACTOR) * 1024)
+    src_hash = library_source_hash()
+    traffic, traffic_note = pmc_traffic(R, C, S, fetch_name, src_hash)
     out = {
         "metric": METRIC,
         "value": ROWS * COLS * 2 / t_rot / 1e3,
@@ -467,13 +550,13 @@ def main():
         "reference_layout": reflayout,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "traffic_source": None if traffic is None else
-                     "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, scaled x2.0 / x1.0 "
-                     "(profiles/rans_w64_gemv_1536x8960_3.25b.md)",
+                     "traffic_source": traffic_note,
+                     "library_source_hash": src_hash,
                      "kernel": "rans_w64_gemv_kernel", "bytes_per_launch": alg},
         "cpu_baseline": cpu,
         "chain": chain,
         "ecsq_wf": ecsq,
+        "configs": configs,
     }
     print(json.dumps(out), flush=True)
 

@@ -47,3 +47,21 @@ def test_rotation_covers_the_caches(nbytes, iters):
         assert (n - 1) * nbytes >= rot
     else:
         assert (n - iters) * nbytes >= rot
+
+
+def test_traffic_only_for_the_measured_sources():
+    """roofline.traffic comes from counters measured on one build: the line
+    carries it only when the library sources hash to the recorded value,
+    and says why otherwise."""
+    sys.path.insert(0, ROOT)
+    import bench
+    h = bench.library_source_hash()
+    assert len(h) == 12 and int(h, 16) >= 0
+    key = next(iter(bench.PMC_TRAFFIC_KIB))
+    rec = bench.PMC_TRAFFIC_KIB[key]
+    t, note = bench.pmc_traffic(*key, rec["source_hash"])
+    assert t == int((rec["fetch_kib"] * 2.0 + rec["write_kib"] * 1.0) * 1024) and "rocprofv3" in note
+    t, note = bench.pmc_traffic(*key, "0" * 12)
+    assert t is None and "measured on library sources" in note
+    t, note = bench.pmc_traffic(1, 64, 1, "refill", h)
+    assert t is None and "tiling" in note

@@ -367,12 +367,18 @@ def chain_tiling(rows, cols):
     return pick_tiling(rows, cols, S=1)
 
 
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak
+
+
 def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None, C=None, S=1,
                   iters=100, rotate_bytes=512 << 20, codes=None, step=None):
     """Times one encoded matrix (rotated over >= rotate_bytes of copies),
     the bf16 F.linear and the library's bf16_gemv on the same shape and
     rotation; checks the GEMV.
-    codes/step: a given matrix and its steps instead of synthetic ones."""
+    codes/step: a given matrix and its steps instead of synthetic ones.
+    batch: rows of x, or a tuple of them (one record per entry, in order,
+    all on the same encoded matrix and copies)."""
+    batches = tuple(batch) if isinstance(batch, (tuple, list)) else (batch,)
     if codes is None:
         codes = synth_codes_full(rows, cols, bits, dist=dist, seed=seed, escape_frac=escape_frac)
         step = torch.from_numpy(lognormal_steps(cols, seed=seed))
@@ -382,44 +388,55 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
         R, C = pick_tiling(rows, cols, S=S, bits=bits)
     enc = encode(codes, R, C, S)
     m = rans.RansMatrix(enc, step, lib)
-    flags = m.tune(batch=batch)
     ncopy = copies_for(iters, m.nbytes, rotate_bytes)
-    ms = [m] + [rans.RansMatrix(enc, step, lib, flags=flags) for _ in range(ncopy - 1)]
-    x = torch.randn(batch, cols, device="cuda").bfloat16()
-    y = torch.empty(batch, rows, device="cuda")
-    t_rans = timeit_graph([lambda mm=mm: mm.gemv(x, y) for mm in ms], iters, rotate=True)
     nW = copies_for(iters, rows * cols * 2, rotate_bytes)
     W = (torch.from_numpy(codes.astype(np.float32)) * step).bfloat16().cuda()
     Ws = [W] + [W.clone() for _ in range(nW - 1)]
-    t_bf16 = timeit_graph([lambda Wd=Wd: torch.nn.functional.linear(x, Wd) for Wd in Ws], iters,
-                          rotate=True)
-    # the library's dense bf16_gemv on the same copies (one vector per launch,
-    # so batch b takes b launches)
     mbs = [rans.Bf16Matrix(Wd, lib) for Wd in Ws]
     yh = torch.empty(rows, device="cuda")
+    Wd64 = torch.from_numpy(codes).cuda().double().t()
+    h = entropy_fast(codes)
+    out = []
+    for b in batches:
+        flags = m.tune(batch=b)
+        ms = [rans.RansMatrix(enc, step, lib, flags=flags) for _ in range(ncopy)]
+        x = torch.randn(b, cols, device="cuda").bfloat16()
+        y = torch.empty(b, rows, device="cuda")
+        t_rans = timeit_graph([lambda mm=mm: mm.gemv(x, y) for mm in ms], iters, rotate=True)
+        t_bf16 = timeit_graph([lambda Wd=Wd: torch.nn.functional.linear(x, Wd) for Wd in Ws],
+                              iters, rotate=True)
 
-    def dense(mb):
-        for b in range(batch):
-            mb.gemv(x[b], yh)
+        # the library's dense bf16_gemv on the same copies (one vector per
+        # launch, so batch b takes b launches)
+        def dense(mb, x=x, b=b):
+            for i in range(b):
+                mb.gemv(x[i], yh)
 
-    t_bf16_hip = timeit_graph([lambda mb=mb: dense(mb) for mb in mbs], iters, rotate=True)
-    del mbs
-    # against the exact product codes @ (x * step) in float64 (the bf16
-    # comparator's weights are themselves rounded)
-    ref = (x.double() * step.double().cuda()) @ torch.from_numpy(codes).cuda().double().t()
-    got = ms[0].gemv(x).double()
-    err = float((got - ref).norm() / ref.norm())
-    out = dict(rows=rows, cols=cols, bits_target=bits, dist=dist, escape_frac=escape_frac,
-               batch=batch, R=R, C=C, S=S, word_fetch={1: "always", 2: "refill"}[flags & 3],
-               entropy=entropy_fast(codes),
-               bits_total=8 * m.nbytes / codes.size, n_escapes=int(len(enc["esc_pos"])),
-               t_rans_us=t_rans, t_bf16_us=t_bf16, t_bf16_hip_us=t_bf16_hip,
-               effective_GBps=rows * cols * 2 / t_rans / 1e3,
-               compressed_GBps=m.nbytes / t_rans / 1e3,
-               speedup_vs_bf16=t_bf16 / t_rans, rel_l2_vs_f64=err, copies=ncopy)
-    del ms, Ws
+        t_bf16_hip = timeit_graph([lambda mb=mb: dense(mb) for mb in mbs], iters, rotate=True)
+        # against the exact product codes @ (x * step) in float64 (the bf16
+        # comparator's weights are themselves rounded)
+        ref = (x.double() * step.double().cuda()) @ Wd64
+        got = ms[0].gemv(x).double()
+        err = float((got - ref).norm() / ref.norm())
+        # bytes one launch must move: the matrix as the device holds it, x
+        # (bf16), the step vector and y (f32)
+        alg = m.nbytes + 2 * cols * b + 4 * cols + 4 * rows * b
+        out.append(dict(rows=rows, cols=cols, bits_target=bits, dist=dist,
+                        escape_frac=escape_frac, batch=b, R=R, C=C, S=S,
+                        word_fetch={1: "always", 2: "refill"}[flags & 3],
+                        entropy=h, bits_total=8 * m.nbytes / codes.size,
+                        n_escapes=int(len(enc["esc_pos"])), t_rans_us=t_rans,
+                        t_bf16_us=t_bf16, t_bf16_hip_us=t_bf16_hip,
+                        effective_GBps=rows * cols * 2 / t_rans / 1e3,
+                        compressed_GBps=m.nbytes / t_rans / 1e3,
+                        compressed_bytes=int(m.nbytes), algorithmic_bytes=int(alg),
+                        roofline_frac=alg / t_rans / 1e3 / HBM_PEAK_GBS,
+                        speedup_vs_bf16=t_bf16 / t_rans, speedup_vs_bf16_hip=t_bf16_hip / t_rans,
+                        rel_l2_vs_f64=err, copies=ncopy, bf16_copies=nW))
+        del ms
+    del mbs, Ws, m
     torch.cuda.empty_cache()
-    return out
+    return out if isinstance(batch, (tuple, list)) else out[0]
 
 
 # projections of a layer that read the same activations
@@ -587,16 +604,15 @@ def configs():
         ("1536x8960 3.25b laplace B8 (one batch-8 launch)", 1536, 8960, 3.25, "laplace", 0.0, 8),
         ("gate/up 2.25b esc0.1%", 8960, 1536, 2.25, "laplace", 0.001, 1),
         ("down 2.25b esc0.1%", 1536, 8960, 2.25, "laplace", 0.001, 1),
-        ("27B 25600x5120 t3 2.25b esc1% B1", 25600, 5120, 2.25, "student3", 0.01, 1),
-        ("27B 25600x5120 t3 2.25b esc1% B4", 25600, 5120, 2.25, "student3", 0.01, 4),
-        ("27B 5120x25600 t3 2.25b esc1% B1", 5120, 25600, 2.25, "student3", 0.01, 1),
-        ("27B 5120x25600 t3 2.25b esc1% B4", 5120, 25600, 2.25, "student3", 0.01, 4),
+        ("27B 25600x5120 t3 2.25b esc1%", 25600, 5120, 2.25, "student3", 0.01, (1, 4)),
+        ("27B 5120x25600 t3 2.25b esc1%", 5120, 25600, 2.25, "student3", 0.01, (1, 4)),
     ]
     for name, rows, cols, bits, dist, esc, batch in cases:
-        r = config_matrix(rows, cols, bits, dist, esc, batch, seed=rows + cols, lib=lib)
-        r["case"] = name
-        print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}),
-              flush=True)
+        rs = config_matrix(rows, cols, bits, dist, esc, batch, seed=rows + cols, lib=lib)
+        for r in (rs if isinstance(rs, list) else [rs]):
+            r["case"] = name if not isinstance(rs, list) else f"{name} B{r['batch']}"
+            print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
+                              for k, v in r.items()}), flush=True)
     # ECSQ-GPTQ + waterfilling code statistics (the k projection's codes of a
     # synthetic layer, tiled to the q/k/v group's shape) with their own steps
     codes, step = ecsq_fixture(rows=2048)
