@@ -22,7 +22,6 @@ Prints one JSON line.  `value` is the bf16-equivalent effective weight
 throughput rows*cols*2 bytes / time per GEMV.
 """
 import argparse
-import hashlib
 import json
 import os
 import sys
@@ -58,15 +57,7 @@ PMC_TRAFFIC_KIB = {(3, 2240, 1, "refill"): dict(source_hash="2ab2e23b36a1",
 PMC_FETCH_FACTOR, PMC_WRITE_FACTOR = 2.0, 1.0
 
 
-def library_source_hash():
-    """First 12 hex digits of the SHA-256 of the library's sources and
-    header (rans.SOURCES, rans.HEADERS, in that order): names the build a
-    counter figure belongs to."""
-    h = hashlib.sha256()
-    for path in rans.SOURCES + rans.HEADERS:
-        with open(path, "rb") as f:
-            h.update(f.read())
-    return h.hexdigest()[:12]
+library_source_hash = B.library_source_hash
 
 
 def pmc_traffic(R, C, S, word_fetch, src_hash):

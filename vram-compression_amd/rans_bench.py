@@ -15,6 +15,7 @@ Timing is done on the device: a launch sequence is captured once in a HIP
 graph and replayed between HIP events, so host dispatch cost (about 10-20 us
 per Python-level call) does not hide a kernel of a few microseconds.
 """
+import hashlib
 import json
 import os
 import sys
@@ -244,10 +245,31 @@ def test():
     print("ok  int4 baseline")
 
 
-def bench(rotate_bytes=512 << 20, iters=200):
-    """bench.py:82-126 on the w64 GEMV: same shapes and rates, same record
-    keys; times are device times of graph-replayed launches over enough
-    distinct copies to exceed the 256 MB Infinity Cache."""
+def library_source_hash():
+    """First 12 hex digits of the SHA-256 of the library's sources and
+    header (rans.SOURCES, rans.HEADERS, in that order): names the build a
+    measurement belongs to."""
+    h = hashlib.sha256()
+    for path in rans.SOURCES + rans.HEADERS:
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:12]
+
+
+BENCH_FILE = "kernel_bench_mi355x.json"
+
+
+def bench(rotate_bytes=512 << 20, iters=200, out_name=BENCH_FILE):
+    """bench.py:82-126 on the w64 GEMV: the same 18 shapes and rates, codes
+    from the same generator and seeds, the same record keys.  Every time is
+    the device time of graph-replayed launches over rotated copies
+    (copies_for: each timed launch reads a copy that at least rotate_bytes
+    of other copies have displaced from the 256 MB Infinity Cache and the
+    L2), for the rANS GEMV, F.linear (t_bf16_us), the library's bf16_gemv
+    (t_bf16_hip_us), the int4 GEMV with its host fold (t_int4_us) and
+    decode-to-bf16 + F.linear (t_decode_then_cublas_us).  The tiling is the
+    library's pick_tiling with one and with two states per lane, the faster
+    kept.  Writes results/<out_name>: {"meta": ..., "records": [...]}."""
     lib = rans.build()
     shapes = {"1.5B qkv": (2048, 1536), "1.5B gate_up": (17920, 1536), "1.5B down": (1536, 8960),
               "27B-like attn": (5120, 5120), "27B-like gate_up": (34816, 5120),
@@ -259,48 +281,64 @@ def bench(rotate_bytes=512 << 20, iters=200):
             step = torch.rand(cols) * 0.01 + 0.005
             x = torch.randn(cols, device="cuda")
             xb = x.bfloat16()
-            nW = max(1, -(-rotate_bytes // (rows * cols * 2)))
-            Ws = [(torch.from_numpy(codes).float() * step).bfloat16().cuda() for _ in range(nW)]
+            nW = copies_for(iters, rows * cols * 2, rotate_bytes)
+            W = (torch.from_numpy(codes).float() * step).bfloat16().cuda()
+            Ws = [W] + [W.clone() for _ in range(nW - 1)]
             t_bf16 = timeit_graph([lambda W=W: torch.nn.functional.linear(xb, W) for W in Ws], iters)
             mbs = [rans.Bf16Matrix(W, lib) for W in Ws]
             yh = torch.empty(rows, device="cuda")
             t_bf16_hip = timeit_graph([lambda mb=mb: mb.gemv(xb, yh) for mb in mbs], iters)
-            del Ws, mbs
-            n4 = max(1, -(-rotate_bytes // (rows * cols // 2)))
+            del Ws, mbs, W
+            n4 = copies_for(iters, rows * cols // 2, rotate_bytes)
             m4 = rans.Int4Matrix(np.clip(codes, -8, 7), step, lib)
             m4s = [m4] + [m4.clone() for _ in range(n4 - 1)]
             y4 = torch.empty(rows, device="cuda")
             t_int4 = timeit_graph([lambda m4=m4: m4.gemv(x, y4) for m4 in m4s], iters)
+            del m4s, m4
             best = None
             for S in (1, 2):
                 R, C = pick_tiling(rows, cols, S=S)
                 enc = rans.encode(codes, R, C, S)
                 m = rans.RansMatrix(enc, step, lib)
-                ncopy = max(1, -(-rotate_bytes // m.nbytes))
+                ncopy = copies_for(iters, m.nbytes, rotate_bytes)
                 ms = [m] + [rans.RansMatrix(enc, step, lib) for _ in range(ncopy - 1)]
                 yb = torch.empty(rows, device="cuda")
                 t = timeit_graph([lambda mm=mm: mm.gemv(xb, yb) for mm in ms], iters)
                 if best is None or t < best["t_rans_us"]:
-                    buf = torch.empty(rows, cols, device="cuda", dtype=torch.bfloat16)
-                    t_dec = timeit_graph(lambda: torch.nn.functional.linear(xb, m.decode(buf)), 20)
-                    best = dict(R=R, C=C, S=S, t_rans_us=t, t_decode_then_cublas_us=t_dec,
-                                bits_total=8 * m.nbytes / codes.size,
+                    best = dict(R=R, C=C, S=S, t_rans_us=t, bits_total=8 * m.nbytes / codes.size,
                                 bits_payload=enc["bits_payload"],
-                                bits_overhead=enc["bits_state_offs"] + enc["bits_table"] + enc["bits_escape"])
-                del ms, m
+                                bits_overhead=enc["bits_state_offs"] + enc["bits_table"] +
+                                enc["bits_escape"], copies=ncopy, _ms=ms)
+                else:
+                    del ms
+                del m
+            ms = best.pop("_ms")
+            buf = torch.empty(rows, cols, device="cuda", dtype=torch.bfloat16)
+            best["t_decode_then_cublas_us"] = timeit_graph(
+                [lambda mm=mm: torch.nn.functional.linear(xb, mm.decode(buf)) for mm in ms], iters)
+            del ms, buf
             r = dict(shape=name, rows=rows, cols=cols, entropy=entropy_fast(codes),
-                     t_bf16_us=t_bf16, t_bf16_hip_us=t_bf16_hip, t_int4_us=t_int4, **best)
+                     t_bf16_us=t_bf16, t_bf16_hip_us=t_bf16_hip, t_int4_us=t_int4, **best,
+                     bf16_copies=nW, int4_copies=n4)
             r["speedup_vs_bf16"] = t_bf16 / r["t_rans_us"]
             r["speedup_vs_bf16_hip"] = t_bf16_hip / r["t_rans_us"]
             r["speedup_vs_int4"] = t_int4 / r["t_rans_us"]
             print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}),
                   flush=True)
             out.append(r)
-            del m4s, m4
             torch.cuda.empty_cache()
+    meta = dict(device=torch.cuda.get_device_name(0),
+                arch=getattr(torch.cuda.get_device_properties(0), "gcnArchName", "gfx950"),
+                torch=torch.__version__, hip=torch.version.hip,
+                library_source_hash=library_source_hash(), iters=iters,
+                rotate_bytes=rotate_bytes,
+                timing="device time per launch of `iters` launches captured in one HIP graph, "
+                       "replayed between HIP events, rotating over distinct copies",
+                workload="kernel/bench.py:26-35 generator (synth_codes, seed rows+cols), one step "
+                         "U[0.005, 0.015) per column, f32 x (bf16 for the bf16 and rANS GEMVs)")
     os.makedirs(RES, exist_ok=True)
-    with open(os.path.join(RES, "kernel_bench.json"), "w") as f:
-        json.dump(out, f, indent=1)
+    with open(os.path.join(RES, out_name), "w") as f:
+        json.dump({"meta": meta, "records": out}, f, indent=1)
 
 
 def bench_reference_layout(rotate_bytes=512 << 20, iters=200, out_name="kernel_bench_reflayout.json"):
