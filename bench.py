@@ -8,9 +8,12 @@ one step chosen so the full tensor's empirical entropy is 3.25 bits, stored
 in the w64 rANS format; log-normal (sigma 0.5) per-column waterfilling steps;
 x ~ N(0,1) in bf16; batch 1.  A step is one GEMV y = codes @ (x*step).
 
-Timing: W warm-up launches, then K launches captured in one HIP graph (so
-Python dispatch cost is not measured) and replayed between HIP events on the
-launch stream.  Launches rotate over distinct encoded copies so that every
+Timing: W warm-up launches, at least 10 ms of untimed replays (the clocks
+ramp up after the host-side encoding), then K launches captured in one HIP graph (so
+Python dispatch cost is not measured) and replayed between two HIP events on
+the launch stream, created with hipEventDisableSystemFence (the default
+events' system-scope cache writeback and invalidate would add ~10 us to the
+timed region).  Launches rotate over distinct encoded copies so that every
 timed launch reads a copy that >= 512 MiB of other copies have passed through
 the caches since its last read: the 256 MB Infinity Cache and the L2 cannot
 serve the compressed stream, whatever K is (with K below the copies 512 MiB
@@ -95,7 +98,8 @@ def copies_for(steps, nbytes):
 
 def graph_time_us(fns, steps, warmup, rotate=None):
     """Device microseconds per call of exactly `steps` calls captured in one
-    HIP graph and replayed between HIP events on the launch stream.
+    HIP graph and replayed between two HIP events on the launch stream
+    (rans_bench.device_elapsed_us: events without the system-scope fence).
 
     rotate (the number of copies the calls in fns rotate over, len(fns)):
     when steps is smaller than that, the timed graph runs calls 0..steps-1
@@ -132,18 +136,15 @@ def graph_time_us(fns, steps, warmup, rotate=None):
     if lead is not None:
         lead.replay()
     torch.cuda.synchronize()
-    # The timed replay is queued while the device still runs the lead-in, so
+    # At least 10 ms of untimed replays of the lead-in (or of the timed graph)
+    # queued back to back bring the clocks to their loaded state, and the
+    # timed replay is queued while the device still runs the last of them, so
     # the start event fires when that work ends and not while the host is
     # still submitting the timed graph: the events time the device's `steps`
-    # launches.  With the device idle at the start event, 20 launches of the
-    # 1536x8960 GEMV read 0.5-0.9 us per launch above their kernel time.
-    (lead if lead is not None else g).replay()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1000.0 / steps
+    # launches (rans_bench.warm_then_time).  With the device idle at the start
+    # event, 20 launches of the 1536x8960 GEMV read 0.5-0.9 us per launch
+    # above their kernel time.
+    return B.warm_then_time(g, lead) / steps
 
 
 def rotation_record(steps, ncopy, nbytes):

@@ -15,6 +15,7 @@ Timing is done on the device: a launch sequence is captured once in a HIP
 graph and replayed between HIP events, so host dispatch cost (about 10-20 us
 per Python-level call) does not hide a kernel of a few microseconds.
 """
+import ctypes
 import hashlib
 import json
 import os
@@ -162,11 +163,86 @@ def copies_for(iters, nbytes, rotate_bytes=512 << 20):
     return n if iters >= n else iters + n
 
 
+# hipEventDisableSystemFence (hip_runtime_api.h): the event records without a
+# system-scope cache writeback and invalidate, which is a cost of the timing
+# event and not of the work it brackets.  On MI355X the default events add
+# ~10 us to a timed region (0.5 us per launch over 20 headline GEMVs, 11.1
+# against 10.6 us; equal at 200).
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+_HIP = None
+
+
+def _hip():
+    global _HIP
+    if _HIP is None:
+        h = ctypes.CDLL("libamdhip64.so")
+        h.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                          ctypes.c_void_p]
+        h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        _HIP = h
+    return _HIP
+
+
+def device_elapsed_us(run):
+    """Device microseconds of the work run() queues on the current stream,
+    between two HIP events recorded on that stream (created with
+    hipEventDisableSystemFence); the host waits for the second."""
+    h = _hip()
+    stream = torch.cuda.current_stream().cuda_stream
+    evs = []
+    try:
+        for _ in range(2):
+            e = ctypes.c_void_p()
+            rc = h.hipEventCreateWithFlags(ctypes.byref(e), HIP_EVENT_DISABLE_SYSTEM_FENCE)
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+            evs.append(e)
+        if h.hipEventRecord(evs[0], stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+        run()
+        if h.hipEventRecord(evs[1], stream) != 0 or h.hipEventSynchronize(evs[1]) != 0:
+            raise RuntimeError("hipEventRecord / hipEventSynchronize failed")
+        ms = ctypes.c_float()
+        if h.hipEventElapsedTime(ctypes.byref(ms), evs[0], evs[1]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value * 1000.0
+    finally:
+        for e in evs:
+            h.hipEventDestroy(e)
+
+
+# Untimed device work queued right before a timed region.  The GPU's clocks
+# ramp up over a few milliseconds of load after an idle spell (the host-side
+# encoding and uploads before each measurement): on MI355X, 20 headline GEMVs
+# timed right after one untimed pass over the rotated copies read 11.2 us,
+# after ~15 ms of untimed passes 10.6 us (25600x5120: 54.3 and 51.5 us).
+WARM_US = 10000.0
+
+
+def warm_then_time(timed, lead=None):
+    """Device microseconds of timed.replay() (a captured graph), after
+    replays of `lead` (default: timed itself), all queued back to back,
+    totalling at least WARM_US of device time; the last lead replay runs
+    just before the timed one, so the start event does not wait for the
+    host to submit it."""
+    lead = lead or timed
+    t_lead = device_elapsed_us(lead.replay)
+    for _ in range(max(1, -(-int(WARM_US) // max(1, int(t_lead))))):
+        lead.replay()
+    t = device_elapsed_us(timed.replay)
+    torch.cuda.synchronize()
+    return t
+
+
 def timeit_graph(fns, iters=200, warmup=10, rotate=False):
     """Device time per call: fns (one callable, or a list cycled through, one
     per rotating copy, sized by copies_for) are captured `iters` times in a
-    HIP graph; the graph is replayed once untimed and then timed between HIP
-    events.  With several copies, an untimed graph runs just before the
+    HIP graph; the graph is replayed once untimed and then, after at least
+    WARM_US of untimed replays (warm_then_time), timed between HIP events.
+    With several copies, an untimed graph runs just before the
     timed replay: the copies the timed graph does not use (iters below
     len(fns)), else every copy once in order, so every timed call reads a
     copy that the other copies have displaced from the caches.  rotate is
@@ -201,15 +277,7 @@ def timeit_graph(fns, iters=200, warmup=10, rotate=False):
     g.replay()
     lead.replay()
     torch.cuda.synchronize()
-    # queued behind the lead-in, so the start event does not wait for the
-    # host to submit the timed graph
-    lead.replay()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    g.replay()
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / iters * 1000
+    return warm_then_time(g, lead) / iters
 
 
 def test():
