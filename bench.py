@@ -274,8 +274,10 @@ def main():
                     help="skip the reference's own 32-lane layout at its published tiling")
     ap.add_argument("--sweep", action="store_true", help="print a tiling sweep to stderr")
     ap.add_argument("--profile", action="store_true",
-                    help="for rocprofv3: K eager launches of the headline GEMV over the rotating "
-                         "copies, then one 256 MiB device copy as the FETCH/WRITE calibration")
+                    help="for rocprofv3: W eager warm-up launches, then K eager launches of the "
+                         "headline GEMV, each on a copy no earlier launch read (the rotation of a "
+                         "timed run with the same --steps), then one 256 MiB elementwise kernel "
+                         "as the FETCH/WRITE calibration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the library has no multi-GPU path "
@@ -318,13 +320,19 @@ def main():
         R, C, S = (int(v) for v in args.tiling.split(",")) if args.tiling else DEFAULT_TILING
         enc = rans.encode(codes, R, C, S)
         comp, alg = algorithmic_bytes(enc, ROWS, COLS)
-        ncopy = max(2, -(-ROTATE_BYTES // comp))
+        # the rotation a timed run of the same --steps uses (copies_for):
+        # every launch below reads a copy no earlier launch read
+        ncopy = copies_for(args.steps, comp)
         m0 = rans.RansMatrix(enc, step_t, lib)
         flags = pick_fetch(m0)
         ms = [m0] + [rans.RansMatrix(enc, step_t, lib, flags=flags) for _ in range(ncopy - 1)]
         y = torch.empty(ROWS, device="cuda")
-        for i in range(args.warmup + args.steps):
-            ms[i % ncopy].gemv(xb, y)
+        # warm-up launches on the copies the profiled ones do not read, then
+        # `steps` launches on copies 0..steps-1
+        for i in range(args.warmup):
+            ms[ncopy - 1 - i % (ncopy - args.steps)].gemv(xb, y)
+        for i in range(args.steps):
+            ms[i].gemv(xb, y)
         torch.cuda.synchronize()
         # calibration: an elementwise kernel that reads and writes 256 MiB
         src = torch.ones(64 << 20, dtype=torch.int32, device="cuda")
@@ -333,7 +341,8 @@ def main():
         torch.neg(src, out=dst)
         torch.cuda.synchronize()
         print(json.dumps({"profile": True, "R": R, "C": C, "S": S, "flags": flags,
-                          "launches": args.warmup + args.steps,
+                          "launches": args.warmup + args.steps, "profiled_launches": args.steps,
+                          "library_source_hash": library_source_hash(),
                           "copies": ncopy, "algorithmic_bytes_per_launch": alg,
                           "compressed_bytes": comp, "calibration_copy_bytes": 256 << 20}), flush=True)
         return
