@@ -55,7 +55,7 @@ DEFAULT_TILING = (3, 2240, 1)
 # profiles/rans_w64_gemv_1536x8960_3.25b.md.  Keyed by (R, C, S, word fetch)
 # and by the hash of the library sources they were measured on
 # (library_source_hash): with other sources the line reports traffic null.
-PMC_TRAFFIC_KIB = {(3, 2240, 1, "refill"): dict(source_hash="2ab2e23b36a1",
+PMC_TRAFFIC_KIB = {(3, 2240, 1, "refill"): dict(source_hash="29fc89a58a82", commit="cc80b17",
                                                 fetch_kib=3445.6, write_kib=12.0)}
 PMC_FETCH_FACTOR, PMC_WRITE_FACTOR = 2.0, 1.0
 
@@ -75,7 +75,7 @@ def pmc_traffic(R, C, S, word_fetch, src_hash):
                       f"these are {src_hash}")
     t = int((pmc["fetch_kib"] * PMC_FETCH_FACTOR + pmc["write_kib"] * PMC_WRITE_FACTOR) * 1024)
     return t, ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, scaled x2.0 / x1.0, "
-               f"measured on library sources {src_hash} "
+               f"measured on library sources {src_hash} at commit {pmc['commit']} "
                "(profiles/rans_w64_gemv_1536x8960_3.25b.md)")
 
 
