@@ -225,12 +225,13 @@ WARM_US = 10000.0
 def warm_then_time(timed, lead=None):
     """Device microseconds of timed.replay() (a captured graph), after
     replays of `lead` (default: timed itself), all queued back to back,
-    totalling at least WARM_US of device time; the last lead replay runs
-    just before the timed one, so the start event does not wait for the
-    host to submit it."""
+    totalling at least WARM_US of device time (at most 1000 replays, so a
+    tiny graph does not turn into a host-bound loop); the last lead replay
+    runs just before the timed one, so the start event does not wait for
+    the host to submit it."""
     lead = lead or timed
     t_lead = device_elapsed_us(lead.replay)
-    for _ in range(max(1, -(-int(WARM_US) // max(1, int(t_lead))))):
+    for _ in range(min(1000, max(1, -(-int(WARM_US) // max(1, int(t_lead)))))):
         lead.replay()
     t = device_elapsed_us(timed.replay)
     torch.cuda.synchronize()
