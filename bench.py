@@ -81,11 +81,12 @@ def pmc_traffic(R, C, S, word_fetch, src_hash):
 
 def algorithmic_bytes(enc, rows, cols, batch=1):
     """Bytes one GEMV must move: the whole compressed matrix as the device
-    holds it (payload and padding words, tile offsets, per-state offsets and
-    initial states, the 32 KB LDS image of the table, the escape side table),
-    x (bf16), the step vector (f32) and y (f32)."""
+    holds it (payload and padding words with each tile's bit-packed initial
+    states, tile offsets and metadata, per-state length and exponent bytes,
+    the 32 KB LDS image of the table, the escape side table), x (bf16), the
+    step vector (f32) and y (f32)."""
     comp = (enc["words"].nbytes + enc["tile_off"].nbytes + enc["slen"].nbytes +
-            enc["states"].nbytes + 2 * enc["table"].nbytes + enc["esc_tileptr"].nbytes +
+            enc["tile_meta"].nbytes + 2 * enc["table"].nbytes + enc["esc_tileptr"].nbytes +
             enc["esc_pos"].nbytes + enc["esc_val"].nbytes)
     return comp, comp + cols * 2 * batch + cols * 4 + rows * 4 * batch
 
@@ -361,7 +362,7 @@ def main():
                         print(f"sweep R={R} C={C} S={S}: {e}", file=sys.stderr)
                         continue
                     bt = 8 * comp / codes.size
-                    print(f"sweep R={R:2d} C={C:5d} S={S} states={len(enc['states']):7d} "
+                    print(f"sweep R={R:2d} C={C:5d} S={S} states={enc['slen'].size:7d} "
                           f"bits_total={bt:.3f} rot={t_rot:7.2f}us hot={t_hot:7.2f}us "
                           f"eff={ROWS * COLS * 2 / t_rot / 1e3:7.1f}GB/s", file=sys.stderr, flush=True)
 
@@ -538,7 +539,7 @@ def main():
         "config": {"workload": f"{ROWS}x{COLS} Laplace ECSQ codes at {BITS} bits/weight entropy, "
                                "log-normal per-column steps, bf16 x, batch 1",
                    "rows": ROWS, "cols": COLS, "batch": 1, "R": R, "C": C, "S": S,
-                   "states": int(len(enc["states"])), "bits_total": bits_total,
+                   "states": int(enc["slen"].size), "bits_total": bits_total,
                    "bits_payload": enc["bits_payload"], "rotating_copies": ncopy,
                    "rotation": rotation_record(args.steps, ncopy, comp),
                    "word_fetch": {1: "always", 2: "refill"}.get(measure.flags & 3, "default"),

@@ -38,13 +38,22 @@
  *     Hence R*C <= 65536 and escape codes within [-32768, 32767].
  *   - words: all tile blocks concatenated; tile t's block is
  *     words[tile_off[t] .. tile_off[t+1]), a multiple of 8 words with at least
- *     one trailing pad word.  The streams of the tile's 64*S states follow
- *     each other in state order, state j's holding slen[t*64*S+j] words (its
- *     renormalisation words in decode order), so it starts at tile_off[t]
- *     plus the lengths of states 0..j-1.  A stream of n symbols has at most
- *     0.75n+1 words (12 bits per symbol at most), so lengths fit a byte for
- *     up to 338 symbols per state (R*C/(64*S)).  states[] holds each
- *     state's initial (decoder) value.
+ *     one trailing pad word.  It opens with the tile's initial decoder states
+ *     (blob_words words), then holds the streams of its 64*S states in state
+ *     order (each state's renormalisation words in decode order).
+ *   - tile_meta[t] = base | blob_words << 16 and, per state j, slen[t*64*S+j]
+ *     = (len_j - base) | e_j << 4: state j's stream is len_j words and starts
+ *     blob_words + len_0 + .. + len_{j-1} words into the block.  Where a
+ *     tile's lengths spread over more than 16 values, the shorter streams are
+ *     padded with zero words (never read) up to base.
+ *   - State j's initial value x_j in [2^16, 2^32) is stored as its exponent
+ *     e_j = floor(log2 x_j) - 16 (in slen) and its 16 + e_j bits below the
+ *     leading one, at bit b_j = (16 + e_0) + .. + (16 + e_{j-1}) of the
+ *     block read as a little-endian bit stream (bit i is bit i%16 of word
+ *     i/16).  32 bits of state and 8 of length became 8 + 16 + e_j bits.
+ *   - A stream of n symbols has at most 0.75n+1 words (12 bits per symbol at
+ *     most); the bases fit a byte for states of up to 338 symbols
+ *     (R*C/(64*S)).
  */
 #ifndef VRAMC_RANS_H
 #define VRAMC_RANS_H
@@ -72,7 +81,8 @@ extern "C" {
 #define RANS_EARG (-4)         /* null pointer or negative size */
 #define RANS_ECODES (-5)       /* encoder: degenerate or empty symbol distribution, or a
                                   code outside [-32768, 32767] */
-#define RANS_ETILE (-6)        /* encoder: a tile block exceeds 65535 words, or a state 255 */
+#define RANS_ETILE (-6)        /* encoder: a tile block exceeds 65535 words, or a tile's
+                                  length base 255 */
 #define RANS_ESCRATCH (-7)     /* rans_w64_gemv_noalloc: the launch needs more split-K
                                   scratch than the library holds (RANS_SCRATCH_BYTES) */
 
@@ -112,8 +122,8 @@ typedef struct rans_w64_matrix {
     int32_t flags;            /* RANS_F_* launch options, 0 for the defaults */
     const uint16_t* words;    /* [tile_off[ntiles]] */
     const uint32_t* tile_off; /* [ntiles+1], in words, multiples of 8 */
-    const uint8_t* slen;      /* [ntiles*64*S], words in each state's stream */
-    const uint32_t* states;   /* [ntiles*64*S] */
+    const uint8_t* slen;      /* [ntiles*64*S], length delta | state exponent << 4 */
+    const uint32_t* tile_meta;/* [ntiles], length base | blob words << 16 */
     const uint32_t* table;    /* [4096], reference packing (host decoder) */
     const uint32_t* table_lds;/* [8192], the table as the kernels hold it in LDS, made
                                  by rans_table_lds from table (device kernels) */
@@ -255,7 +265,7 @@ int rans_table_lds4(const uint32_t* table, uint32_t* out);
  * encode() (rans.py:62-98).  R*C <= 65536 (the side table's 16-bit
  * positions), else RANS_EGEOMETRY; RANS_ECODES for a code outside
  * [-32768, 32767] (the side table's 16-bit values); RANS_ETILE when a tile block
- * exceeds 65535 words or a state's stream 255 words.  On success *handle
+ * exceeds 65535 words or a tile's length base 255 words.  On success *handle
  * owns the result and info[]
  * receives {nwords, ntiles, nstates, nesc, max_tile_words, payload_words,
  * max_state_words}.
@@ -263,8 +273,8 @@ int rans_table_lds4(const uint32_t* table, uint32_t* out);
 int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols, int32_t R, int32_t C,
                     int32_t S, int32_t nthreads, void** handle, int64_t* info);
 
-int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off, uint8_t* slen,
-                          uint32_t* states, uint32_t* table, int64_t* freq,
+int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off,
+                          uint32_t* tile_meta, uint8_t* slen, uint32_t* table, int64_t* freq,
                           int32_t* esc_tileptr, uint16_t* esc_pos, int16_t* esc_val);
 
 /* The symbol counts over the encoded matrix (256 x int64, symbol = code+128,
@@ -277,8 +287,9 @@ void rans_w64_encode_free(void* handle);
 /* Host decoder of the w64 format to int32 codes (escapes applied); replaces
  * decode_ref (rans.py:101-123).  Returns state+1 (positive) for the first
  * state whose final value is not 2^16 (the reference's final-state assert,
- * rans.py:121), RANS_EARG on a stream overrun or an escape side table that
- * disagrees with the escape symbols in the stream. */
+ * rans.py:121), RANS_EARG on a stream overrun, a stream read to other than
+ * its stored length (short only where padded to its tile's base), or an
+ * escape side table that disagrees with the escape symbols in the stream. */
 int rans_w64_decode_host(const rans_w64_matrix* m_host, int32_t* out);
 
 /* The reference's encoder for its own 32-lane layout (kernel/rans.py:62-98),

@@ -273,13 +273,28 @@ def w64_decode(enc):
     ntiles = (rows // R) * (cols // C)
     nst = 64 * S
     n = (C // nst) * R
-    # streams follow each other in state order within a tile block
-    slen = enc["slen"].astype(np.int64).reshape(ntiles, nst)
-    starts_in_tile = np.cumsum(slen, axis=1) - slen
+    w = np.ascontiguousarray(enc["words"], np.uint16)
+    # a tile block opens with its states' initial values, each as 16 + e
+    # bits below an implicit leading one (e in the high half of the state's
+    # slen byte), bit-packed in state order (bit i of the block is bit i%16
+    # of its word i/16); blob_words (tile_meta >> 16) words of them, then the
+    # streams in state order, each base (tile_meta & 255) + (slen & 15) words
+    meta = enc["tile_meta"].astype(np.int64)[:ntiles]
+    sl = enc["slen"].astype(np.int64).reshape(ntiles, nst)
+    nb = 16 + (sl >> 4)
+    bit0 = tile_off[:ntiles, None] * 16 + np.cumsum(nb, axis=1) - nb
+    if np.any(np.cumsum(nb, axis=1)[:, -1] > 16 * (meta >> 16)):
+        raise AssertionError("initial states overrun their tile's blob")
+    mant = np.zeros((ntiles, nst), np.int64)
+    for i in range(31):
+        b = bit0 + i
+        bitv = (w[np.minimum(b >> 4, w.size - 1)].astype(np.int64) >> (b & 15)) & 1
+        mant |= np.where(i < nb, bitv << i, 0)
+    st0 = (mant | (np.int64(1) << nb)).ravel().astype(np.uint32)
+    slen = (meta & 0xFF)[:, None] + (sl & 15)
+    starts_in_tile = (meta >> 16)[:, None] + np.cumsum(slen, axis=1) - slen
     start = (tile_off[:ntiles, None] + starts_in_tile).ravel()
     out = np.zeros((ntiles * nst, n), np.uint8)
-    w = np.ascontiguousarray(enc["words"], np.uint16)
-    st0 = np.ascontiguousarray(enc["states"], np.uint32)
     start = np.ascontiguousarray(start, np.int64)
     rc = lib.orc_decode_streams(_p(w), w.size, _p(st0), _p(start), ntiles * nst, n,
                                 _p(np.ascontiguousarray(enc["table"], np.uint32)), _p(out))

@@ -51,13 +51,13 @@ codes = np.clip(np.round(rng.laplace(size=(64, 256)) * 3), -127, 127).astype(np.
 enc = rans.encode(codes, 4, 256)
 for k in range(30):
     bad = dict(enc, words=enc["words"].copy(), slen=enc["slen"].copy(),
-               states=enc["states"].copy(), esc_pos=enc["esc_pos"].copy())
+               tile_meta=enc["tile_meta"].copy(), esc_pos=enc["esc_pos"].copy())
     if k % 3 == 0:
         bad["words"][rng.integers(0, bad["words"].size)] ^= 0xFFFF
     elif k % 3 == 1:
         bad["slen"][rng.integers(0, bad["slen"].size)] = rng.integers(0, 256)
     else:
-        bad["states"][rng.integers(0, bad["states"].size)] ^= 0xFFFFFFFF
+        bad["tile_meta"][rng.integers(0, bad["tile_meta"].size)] ^= 0xFFFFFFFF
     try:
         rans.decode_ref(bad)
     except AssertionError:

@@ -33,7 +33,7 @@ def _desc(rans, rows=256, cols=4096, R=8, C=256, S=1, mtw=1024):
     fake = 0x1000  # never dereferenced: every call below returns before launching
     return rans.RansMatrixDesc(rows=rows, cols=cols, R=R, C=C, S=S, max_tile_words=mtw,
                                max_state_words=64,
-                               words=fake, tile_off=fake, slen=fake, states=fake, table=fake,
+                               words=fake, tile_off=fake, slen=fake, tile_meta=fake, table=fake,
                                table_lds=fake,
                                esc_tileptr=fake, esc_pos=fake, esc_val=fake, step=fake,
                                workspace=None, workspace_bytes=0)

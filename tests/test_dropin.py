@@ -59,15 +59,16 @@ def _check_enc(rans, enc, codes, R, C):
         assert tC <= 2 * C
     assert tR * tC <= 65536 and tR * tC // (64 * tS) <= rans.MAX_STATE_SYMBOLS
     # offs: one word offset per state (the reference's per-lane offs), each
-    # at its state's stream, which holds slen words, in state order
+    # at its state's stream, in state order after the tile's initial states
     nstates = (rows // tR) * (scols // tC) * 64 * tS
     assert enc["offs"].dtype == np.uint32 and enc["offs"].size == nstates
-    ends = enc["offs"].astype(np.int64) + enc["slen"]
+    ends = enc["offs"].astype(np.int64) + rans.stream_lengths(enc)
     ntiles = (rows // tR) * (scols // tC)
     per_tile = ends.reshape(ntiles, -1)
     starts = enc["offs"].astype(np.int64).reshape(ntiles, -1)
     np.testing.assert_array_equal(starts[:, 1:], per_tile[:, :-1])
-    np.testing.assert_array_equal(starts[:, 0], enc["tile_off"][:-1])
+    np.testing.assert_array_equal(starts[:, 0],
+                                  enc["tile_off"][:-1] + (enc["tile_meta"] >> 16))
     assert np.all(per_tile[:, -1] < enc["tile_off"][1:])  # the pad word follows
     assert np.array_equal(rans.decode_ref(enc), codes)
 

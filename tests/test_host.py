@@ -51,15 +51,25 @@ def test_streams_equal_reference_encoder(rans, oracle, shape):
     assert lib.orc_encode_lanes(p(seqs), lanes, n, p(freq), p(cum), p(words), cap, p(offs)) == 0
     assert lib.orc_count_words(p(seqs), lanes, n, p(freq), p(cum), p(counts)) == 0
     nst = 64 * S
-    # each state's stored length is its stream's word count, and the
-    # streams of a tile follow each other from the tile's offset
-    np.testing.assert_array_equal(enc["slen"], counts)
+    # each state's stored length is its stream's word count, or its tile's
+    # base where the tile's counts spread over more than 16 values (the
+    # shorter streams padded up to it)
+    ntiles = lanes // nst
+    cnt = counts.reshape(ntiles, nst)
+    base = np.maximum(cnt.min(axis=1), cnt.max(axis=1) - 15)
+    np.testing.assert_array_equal(enc["tile_meta"] & 0xFF, base)
+    np.testing.assert_array_equal(rans.stream_lengths(enc),
+                                  np.maximum(cnt, base[:, None]).ravel())
+    # the initial states read back from the tiles' bit-packed mantissas,
+    # and the streams at the offsets the lengths give
+    st0 = rans.initial_states(enc)
+    starts = rans.stream_offsets(enc)
     for j in range(lanes):
         o = int(offs[j])
-        assert int(enc["states"][j]) == (int(words[o]) << 16) | int(words[o + 1])
+        assert int(st0[j]) == (int(words[o]) << 16) | int(words[o + 1])
+        assert (int(enc["slen"][j]) >> 4) == int(st0[j]).bit_length() - 17
         ref_words = words[o + 2:o + 2 + counts[j]]
-        t = j // nst
-        start = int(enc["tile_off"][t]) + int(counts[t * nst:j].sum())
+        start = int(starts[j])
         np.testing.assert_array_equal(enc["words"][start:start + counts[j]], ref_words)
 
 
@@ -114,12 +124,25 @@ def test_escape_side_table_must_match_stream(rans, oracle):
             oracle.w64_decode(bad)
 
 
+def state_bit(enc, t, j):
+    """Absolute bit offset (in enc["words"] read as a little-endian bit
+    stream) of the initial-state mantissa of state j of tile t."""
+    ntiles = enc["tile_off"].size - 1
+    nb = 16 + (enc["slen"].astype(np.int64).reshape(ntiles, -1)[t] >> 4)
+    return int(enc["tile_off"][t]) * 16 + int(nb[:j].sum())
+
+
+def flip_bit(words, bit):
+    words[bit >> 4] ^= np.uint16(1 << (bit & 15))
+
+
 def test_corrupt_state_detected(rans, oracle):
+    """A flipped bit in a state's stored initial value (a low mantissa bit of
+    state 0) is caught by the final-state check of both decoders."""
     codes = oracle.synth_codes(64, 256, 3.0, seed=4)
     enc = rans.encode(codes, 4, 256, 1)
-    bad = dict(enc)
-    bad["states"] = enc["states"].copy()
-    bad["states"][0] ^= 0x5A5A
+    bad = dict(enc, words=enc["words"].copy())
+    flip_bit(bad["words"], state_bit(enc, 0, 0) + 3)
     with pytest.raises(AssertionError):
         rans.decode_ref(bad)
     with pytest.raises(AssertionError):
@@ -133,9 +156,9 @@ def test_first_failing_tile_is_reported(rans, oracle):
     codes = oracle.synth_codes(256, 1024, 3.0, seed=17)
     enc = rans.encode(codes, 8, 256, 1)
     nst = 64
-    bad = dict(enc, states=enc["states"].copy())
-    bad["states"][9 * nst + 5] ^= 0x1234   # tile 9, state 5
-    bad["states"][3 * nst + 40] ^= 0x777   # tile 3, state 40: reported
+    bad = dict(enc, words=enc["words"].copy())
+    flip_bit(bad["words"], state_bit(enc, 9, 5) + 2)    # tile 9, state 5
+    flip_bit(bad["words"], state_bit(enc, 3, 40) + 7)   # tile 3, state 40: reported
     keep = []
     d = rans._host_desc(bad, keep)
     out = np.zeros(codes.shape, np.int32)
@@ -163,8 +186,9 @@ def test_encode_rejects_bad_input(rans):
         wide_code[3, 5] = v
         with pytest.raises(AssertionError, match="32767"):
             rans.encode(wide_code, 4, 128)
-    # a state's stream beyond 255 words (1024 symbols of ~8 bits each) when
-    # the caller fixes one state per lane on a tile the format holds
+    # streams beyond 255 words (1024 symbols of ~8 bits each: a tile's
+    # length base does not fit its byte) when the caller fixes one state per
+    # lane on a tile the format holds
     wide = np.random.default_rng(2).integers(-127, 128, size=(16, 4096)).astype(np.int32)
     with pytest.raises(AssertionError, match="255"):
         rans.encode(wide, 16, 4096, S=1)
@@ -196,12 +220,12 @@ def test_encode_maps_oversized_requests(rans):
 
 
 def test_stream_lengths_must_match(rans, oracle):
+    """A stored length one word off (state 0's, so state 1 also starts one
+    word off) is caught by both decoders."""
     codes = oracle.synth_codes(64, 256, 3.0, seed=5)
     enc = rans.encode(codes, 4, 256, 1)
-    assert enc["slen"][0] > 0
     bad = dict(enc, slen=enc["slen"].copy())
-    bad["slen"][0] -= 1  # state 1 then starts a word early
-    bad["slen"][1] += 1
+    bad["slen"][0] ^= 1  # the low bit of the length delta
     with pytest.raises(AssertionError):
         rans.decode_ref(bad)
     with pytest.raises(AssertionError):
@@ -285,9 +309,16 @@ def test_bit_accounting(rans, oracle):
     nstates = seqs.shape[0]
     ntiles = (rows // R) * (cols // C)
     pad = len(enc["words"]) - counts.sum()
-    assert enc["bits_state_offs"] == (40 * nstates + 32 * (ntiles + 1) + 16 * pad) / N
+    assert enc["bits_state_offs"] == (8 * nstates + 32 * (2 * ntiles + 1) + 16 * pad) / N
     assert enc["bits_table"] == 32 * 4096 / N
-    assert 0 < pad <= 8 * ntiles
+    # the words beyond the payload: each tile's bit-packed initial states
+    # (16 + e bits per state, rounded up to words), the streams padded up to
+    # their tile's length base, and 1 to 8 words closing each block
+    e = enc["slen"].astype(np.int64).reshape(ntiles, -1) >> 4
+    blob = (np.sum(16 + e, axis=1) + 15) // 16
+    np.testing.assert_array_equal(enc["tile_meta"] >> 16, blob)
+    lpad = rans.stream_lengths(enc).sum() - counts.sum()
+    assert ntiles <= pad - blob.sum() - lpad <= 8 * ntiles
     assert np.all(np.diff(enc["tile_off"].astype(np.int64)) % 8 == 0)
     # model entropy (from the encoder's symbol counts) against the direct mean
     direct = -np.log2(freq[sym.ravel()] / 4096).mean()
@@ -304,7 +335,8 @@ def test_encoder_threads_identical(rans, oracle):
     a = rans.encode(codes, 8, 512, 1, threads=1)
     for th in (3, 8):
         b = rans.encode(codes, 8, 512, 1, threads=th)
-        for k in ("words", "tile_off", "slen", "states", "table", "esc_tileptr", "esc_pos", "esc_val"):
+        for k in ("words", "tile_off", "slen", "tile_meta", "table", "esc_tileptr", "esc_pos",
+                  "esc_val"):
             np.testing.assert_array_equal(a[k], b[k])
         assert a["entropy_model"] == b["entropy_model"]
 
@@ -341,7 +373,7 @@ def test_w64_format_golden(rans):
         codes = g[f"{name}_codes"].astype(np.int32)
         assert codes.shape == (rows, cols)
         enc = rans.encode(codes, R, C, S)
-        for k in ("words", "tile_off", "slen", "states", "esc_tileptr", "esc_pos", "esc_val"):
+        for k in ("words", "tile_off", "tile_meta", "slen", "esc_tileptr", "esc_pos", "esc_val"):
             np.testing.assert_array_equal(enc[k], g[f"{name}_{k}"], err_msg=f"{name}.{k}")
         assert (enc["max_tile_words"], enc["max_state_words"]) == (mtw, msw)
         np.testing.assert_array_equal(rans.decode_ref(enc), codes)

@@ -20,7 +20,7 @@ def entries(rans, oracle):
     return out
 
 
-KEYS = ("words", "tile_off", "slen", "states", "table", "esc_tileptr", "esc_pos", "esc_val")
+KEYS = ("words", "tile_off", "slen", "tile_meta", "table", "esc_tileptr", "esc_pos", "esc_val")
 SCALARS = ("R", "C", "S", "shape", "max_tile_words", "max_state_words", "bits_payload",
            "bits_state_offs", "bits_table", "bits_escape")
 
@@ -93,30 +93,29 @@ def test_save_rejects_inconsistent_entries(rans, tmp_path, entries):
         rans_io.save(str(tmp_path / "x.w64"), [e])
 
 
-def test_version_5_written_and_4_read(rans, tmp_path, entries):
-    """The writer stamps version 5; a version-4 file (the same layout, the
-    appended-columns slot zero) still loads; other versions are refused."""
+def test_version_6_written_and_earlier_refused(rans, tmp_path, entries):
+    """The writer stamps version 6; files of the earlier stream layouts
+    (versions 1 to 5) and unknown versions are refused with a ValueError
+    naming the version."""
     import rans_io
     path = str(tmp_path / "set.w64")
     rans_io.save(path, entries)
     raw = bytearray(open(path, "rb").read())
-    assert int.from_bytes(raw[8:12], "little") == rans_io.VERSION == 5
-    for version, ok in ((4, True), (3, False), (6, False)):
+    assert int.from_bytes(raw[8:12], "little") == rans_io.VERSION == 6
+    got = rans_io.load(path)
+    for e, g in zip(entries, got):
+        np.testing.assert_array_equal(rans.decode_ref(g["enc"]), e["codes"])
+    for version in (4, 5, 7):
         p = str(tmp_path / f"v{version}.w64")
         raw[8:12] = version.to_bytes(4, "little")
         open(p, "wb").write(raw)
-        if ok:
-            got = rans_io.load(p)
-            for e, g in zip(entries, got):
-                np.testing.assert_array_equal(rans.decode_ref(g["enc"]), e["codes"])
-        else:
-            with pytest.raises(ValueError, match="version"):
-                rans_io.load(p)
+        with pytest.raises(ValueError, match="version"):
+            rans_io.load(p)
 
 
 def test_appended_columns_round_trip(rans, oracle, tmp_path):
     """A matrix whose cols is an odd multiple of 32 (stored with 32 appended
-    columns) keeps its own shape, step and codes through a version-5 file,
+    columns) keeps its own shape, step and codes through a container file,
     next to one without appended columns."""
     import rans_io
     odd = oracle.synth_codes(64, 224, 3.0, seed=11)

@@ -16,7 +16,7 @@ def _fake_desc(rans, rows, cols, R, C):
     fake = 0x1000  # never dereferenced: the calls below return before launching
     return rans.RansMatrixDesc(rows=rows, cols=cols, R=R, C=C, S=1, max_tile_words=1024,
                                max_state_words=64, words=fake, tile_off=fake, slen=fake,
-                               states=fake, table=fake, table_lds=fake, esc_tileptr=fake,
+                               tile_meta=fake, table=fake, table_lds=fake, esc_tileptr=fake,
                                esc_pos=fake, esc_val=fake, step=fake, workspace=None,
                                workspace_bytes=0)
 

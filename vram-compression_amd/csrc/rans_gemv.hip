@@ -95,8 +95,8 @@ constexpr int kMaxGroup = 4;
 struct MatArgs {
     const uint16_t* words;
     const uint32_t* tile_off;
-    const uint8_t* slen;
-    const uint32_t* states;
+    const uint8_t* slen;        // length delta | state exponent << 4
+    const uint32_t* tile_meta;  // length base | blob words << 16
     const uint4* table_lds;  // 2048 x 16 B LDS image of the table
     const int32_t* esc_tileptr;
     const uint16_t* esc_pos;  // tile-local index c*R + r
@@ -128,7 +128,7 @@ struct DecodeArgs {
     const uint16_t* words;
     const uint32_t* tile_off;
     const uint8_t* slen;
-    const uint32_t* states;
+    const uint32_t* tile_meta;
     const uint4* table_lds;
     const int32_t* esc_tileptr;
     const uint16_t* esc_pos;  // tile-local index c*R + r
@@ -328,18 +328,39 @@ __device__ __forceinline__ uint32_t wave_scan(uint32_t v) {
     return v;
 }
 
-// Word offset of each of the lane's S states within the tile block: the
-// block holds the 64*S streams in state order (j = s*64 + lane), so state
-// j starts after the lengths of states 0..j-1.
+// Where each of the lane's S states lives in the tile block, from its
+// length byte lb (length - base | exponent << 4) and the tile's meta word
+// (base | blob words << 16): off, the word offset of its stream (the
+// streams follow the blob in state order, j = s*64 + lane), and bit, the
+// bit offset of its initial state's mantissa in the blob (16 + e bits per
+// state, in state order).  Both sums go through one scan, packed in the two
+// halves of a word (a wave's lengths stay below 2^16 words and its
+// mantissas below 2^11 bits).
 template <int S>
-__device__ __forceinline__ void stream_offsets(const uint32_t (&len)[S], uint32_t (&off)[S]) {
-    uint32_t carry = 0;
+__device__ __forceinline__ void stream_layout(const uint32_t (&lb)[S], uint32_t meta,
+                                              uint32_t (&off)[S], uint32_t (&bit)[S]) {
+    const uint32_t base = meta & 0xFFu;
+    uint32_t ocarry = meta >> 16, bcarry = 0;
 #pragma unroll
     for (int s = 0; s < S; s++) {
-        const uint32_t inc = wave_scan(len[s]);
-        off[s] = carry + inc - len[s];
-        carry += __builtin_amdgcn_readlane(inc, 63);
+        const uint32_t v = (base + (lb[s] & 15u)) | (16u + (lb[s] >> 4)) << 16;
+        const uint32_t inc = wave_scan(v);
+        const uint32_t ex = inc - v;
+        off[s] = ocarry + (ex & 0xFFFFu);
+        bit[s] = bcarry + (ex >> 16);
+        const uint32_t tot = __builtin_amdgcn_readlane(inc, 63);
+        ocarry += tot & 0xFFFFu;
+        bcarry += tot >> 16;
     }
+}
+
+// A state's initial value from the staged blob: the 16 + e bits at bit
+// offset `bit` below an implicit leading one.
+__device__ __forceinline__ uint32_t initial_state(const uint16_t* raw, uint32_t bit, uint32_t lb) {
+    const uint32_t* r32 = reinterpret_cast<const uint32_t*>(raw);
+    const uint32_t lo = r32[bit >> 5], hi = r32[(bit >> 5) + 1];
+    const uint32_t nb = 16u + (lb >> 4);
+    return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(hi, lo, bit & 31u), 0, nb) | (1u << nb);
 }
 
 // Per-lane decoder state of S interleaved rANS states, with the table entry
@@ -475,7 +496,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves)
     const MatArgs& m = a.mat[GROUP ? mi : 0];
     // Every kernel argument the prologue needs, fetched in one scalar batch
     // (otherwise each is loaded, and waited for, at its first use).
-    asm volatile("" ::"s"(m.tile_off), "s"(m.states), "s"(m.slen), "s"(m.table_lds),
+    asm volatile("" ::"s"(m.tile_off), "s"(m.tile_meta), "s"(m.slen), "s"(m.table_lds),
                  "s"(m.words), "s"(a.x), "s"(m.step), "s"(m.esc_tileptr), "s"(m.esc_pos),
                  "s"(m.esc_val), "s"(m.C), "s"(a.cols),
                  "s"(m.raw_words), "s"(a.W), "s"(m.ncb), "s"(a.ngroups), "s"(a.nb));
@@ -500,12 +521,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves)
     // This tile's range of the escape side table (lanes 0, 1), also needed early.
     const int tp = m.esc_tileptr[t + min(lane, 1)];
     asm volatile("" ::: "memory");  // keep these two loads first
-    uint32_t st0[S], len0[S];
+    const uint32_t tmv = m.tile_meta[t];
+    uint32_t len0[S];
 #pragma unroll
-    for (int s = 0; s < S; s++) {
-        st0[s] = m.states[t * nst + 64 * s + lane];
-        len0[s] = m.slen[t * nst + 64 * s + lane];
-    }
+    for (int s = 0; s < S; s++) len0[s] = m.slen[t * nst + 64 * s + lane];
     // x and step for KU column steps are loaded one block ahead of use, so
     // their latency overlaps the decode of the current block.  They are
     // buffer loads ranged to one x row / the step vector: a block's columns
@@ -623,8 +642,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves)
 
     {
         Lanes<S, TabEntry<T4>> L;
-        uint32_t off0[S];
-        stream_offsets<S>(len0, off0);
+        uint32_t off0[S], bit0[S], st0[S];
+        stream_layout<S>(len0, __builtin_amdgcn_readfirstlane(tmv), off0, bit0);
+#pragma unroll
+        for (int s = 0; s < S; s++) st0[s] = initial_state(raw, bit0[s], len0[s]);
         init_lanes(L, tab, raw, st0, off0);
         for (int k0 = 0; k0 < nk; k0 += KU) {
             convert();
@@ -836,19 +857,17 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
     const bool active = t < a.ntiles;
     const int tc = active ? t : a.ntiles - 1;
     const int rb = tc / a.ncb, cb = tc - rb * a.ncb;
-    asm volatile("" ::"s"(a.tile_off), "s"(a.states), "s"(a.slen), "s"(a.table_lds),
+    asm volatile("" ::"s"(a.tile_off), "s"(a.tile_meta), "s"(a.slen), "s"(a.table_lds),
                  "s"(a.words), "s"(a.step), "s"(a.esc_tileptr), "s"(a.out), "s"(a.C),
                  "s"(a.cols), "s"(a.L.raw_words), "s"(a.W), "s"(a.ncb), "s"(a.ntiles));
 
     const TileOff to = load_tile_off(a.tile_off, tc);
     const int tp = a.esc_tileptr[tc + min(lane, 1)];
     asm volatile("" ::: "memory");  // keep these two loads first
-    uint32_t st0[S], len0[S];
+    const uint32_t tmv = a.tile_meta[tc];
+    uint32_t len0[S];
 #pragma unroll
-    for (int s = 0; s < S; s++) {
-        st0[s] = a.states[tc * nst + 64 * s + lane];
-        len0[s] = a.slen[tc * nst + 64 * s + lane];
-    }
+    for (int s = 0; s < S; s++) len0[s] = a.slen[tc * nst + 64 * s + lane];
     const int nk = a.C / nst;
     const int colbase = cb * a.C + lane;
     const __amdgpu_buffer_rsrc_t srs =
@@ -876,8 +895,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeA
     const __amdgpu_buffer_rsrc_t ors =
         __builtin_amdgcn_make_buffer_rsrc(obase, 0, R * a.cols * ESZ, kBufWord3);
     Lanes<S, TabEntry<false>> L;
-    uint32_t off0[S];
-    stream_offsets<S>(len0, off0);
+    uint32_t off0[S], bit0[S], st0[S];
+    stream_layout<S>(len0, __builtin_amdgcn_readfirstlane(tmv), off0, bit0);
+#pragma unroll
+    for (int s = 0; s < S; s++) st0[s] = initial_state(raw, bit0[s], len0[s]);
     init_lanes(L, tab, raw, st0, off0);
     // One block of nu <= KU column steps.  The loop below runs whole blocks
     // only (nu = KU, no early exit): exits after 1, 2 or 3 steps' stores
@@ -1212,7 +1233,7 @@ bool valid_geometry(const rans_w64_matrix* m) {
 }
 
 bool valid_pointers(const rans_w64_matrix* m) {
-    return m->words && m->tile_off && m->slen && m->states && m->table_lds && m->step &&
+    return m->words && m->tile_off && m->slen && m->tile_meta && m->table_lds && m->step &&
            m->esc_tileptr && m->esc_pos && m->esc_val;
 }
 
@@ -1484,7 +1505,7 @@ int launch_decode_common(const rans_w64_matrix* m, void* out, hipStream_t stream
     a.words = m->words;
     a.tile_off = m->tile_off;
     a.slen = m->slen;
-    a.states = m->states;
+    a.tile_meta = m->tile_meta;
     a.table_lds = reinterpret_cast<const uint4*>(m->table_lds);
     a.esc_tileptr = m->esc_tileptr;
     a.esc_pos = m->esc_pos;
@@ -1610,7 +1631,7 @@ int launch_gemv_common(const rans_w64_matrix* const* ms, int n, const void* x, i
         d.words = m->words;
         d.tile_off = m->tile_off;
         d.slen = m->slen;
-        d.states = m->states;
+        d.tile_meta = m->tile_meta;
         d.table_lds = reinterpret_cast<const uint4*>(m->table_lds);
         d.esc_tileptr = m->esc_tileptr;
         d.esc_pos = m->esc_pos;

@@ -24,9 +24,8 @@ constexpr int kEsc = 0;
 struct Encoded {
     std::vector<uint16_t> words;
     std::vector<uint32_t> tile_off;
-    std::vector<uint16_t> soffs;  // stream starts within the tile block (encoder only)
-    std::vector<uint8_t> slen;    // stream lengths, the stored form
-    std::vector<uint32_t> states;
+    std::vector<uint32_t> tile_meta;  // per tile: length base | blob words << 16
+    std::vector<uint8_t> slen;        // per state: length - base | state exponent << 4
     uint32_t table[kM];
     int64_t freq[256];
     int64_t counts[256] = {0};  // symbol counts over the matrix
@@ -37,6 +36,19 @@ struct Encoded {
     int32_t max_tile_words = 0;
     int32_t max_state_words = 0;  // longest state stream, counting the tile padding
 };
+
+// Initial decoder state x (in [2^16, 2^32)) as its exponent e = floor(log2 x)
+// - 16 (0..15) and the 16 + e bits below its leading one.
+int state_exponent(uint32_t x) { return 31 - __builtin_clz(x) - 16; }
+
+// Appends the low n bits of v (n <= 31) to a little-endian bit stream of
+// 16-bit words at bit offset pos.
+void put_bits(std::vector<uint16_t>& w, size_t first, uint64_t pos, uint32_t v, int n) {
+    for (int i = 0; i < n; i++, pos++) {
+        const size_t k = first + (size_t)(pos >> 4);
+        if ((v >> i) & 1u) w[k] |= (uint16_t)(1u << (pos & 15));
+    }
+}
 
 // Runs fn(i) for i in [0, n) on up to nthreads threads, static blocks.
 template <typename F>
@@ -182,9 +194,8 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
     const int64_t n = (int64_t)nk * R;  // symbols per state
 
     std::vector<std::vector<uint16_t>> blocks((size_t)ntiles);
-    E->soffs.assign((size_t)(ntiles * nst), 0);
+    E->tile_meta.assign((size_t)ntiles, 0);
     E->slen.assign((size_t)(ntiles * nst), 0);
-    E->states.assign((size_t)(ntiles * nst), 0);
     std::vector<int64_t> payload((size_t)ntiles, 0);
     std::vector<int> too_big((size_t)ntiles, 0);
     std::vector<int32_t> longest((size_t)ntiles, 0);
@@ -196,8 +207,9 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
         const int32_t rb = (int32_t)(t / ncb), cb = (int32_t)(t % ncb);
         std::vector<uint8_t> seq((size_t)n);
         std::vector<uint16_t> emitted((size_t)n);
-        std::vector<uint16_t>& blk = blocks[(size_t)t];
-        blk.reserve((size_t)(n * nst / 4 + 16));
+        // each state's words in decode order and its initial decoder state
+        std::vector<std::vector<uint16_t>> dec((size_t)nst);
+        std::vector<uint32_t> x0((size_t)nst);
         for (int32_t j = 0; j < nst; j++) {
             const int32_t s = j / 64, l = j % 64;
             int64_t i = 0;
@@ -219,29 +231,56 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
                 }
                 x = ((x / f) << kScaleBits) + (x % f) + c;
             }
-            const size_t sid = (size_t)(t * nst + j);
-            if (blk.size() > 65535) too_big[(size_t)t] = 1;
-            E->soffs[sid] = (uint16_t)blk.size();
-            if (cnt > 255) too_big[(size_t)t] = 1;
-            E->slen[sid] = (uint8_t)cnt;
-            E->states[sid] = x;
-            for (int64_t q = cnt - 1; q >= 0; q--) blk.push_back(emitted[(size_t)q]);
+            x0[(size_t)j] = x;
+            std::vector<uint16_t>& d = dec[(size_t)j];
+            d.resize((size_t)cnt);
+            for (int64_t q = 0; q < cnt; q++) d[(size_t)q] = emitted[(size_t)(cnt - 1 - q)];
             payload[(size_t)t] += cnt;
         }
-        // At least one pad word (the decoder prefetches one word past the
-        // last one it consumes), then round up to 8 words (16-byte loads).
+        // Lengths against the tile's base: each stored length is base + a
+        // 4-bit delta, so where the lengths spread over more than 16 values
+        // the streams below max - 15 are padded with zero words (never read)
+        // up to it.
+        int32_t lo = INT32_MAX, hi = 0;
+        for (const auto& d : dec) {
+            lo = std::min(lo, (int32_t)d.size());
+            hi = std::max(hi, (int32_t)d.size());
+        }
+        const int32_t base = std::max(lo, hi - 15);
+        if (base > 255) too_big[(size_t)t] = 1;
+        // Block: the initial states' mantissas bit-packed (state j's 16 + e_j
+        // bits after those of states 0..j-1, little endian), then the
+        // streams in state order, then at least one pad word (the decoder
+        // reads one word ahead), rounded up to 8 words (16-byte loads).
+        uint64_t nbits = 0;
+        for (int32_t j = 0; j < nst; j++) nbits += 16 + state_exponent(x0[(size_t)j]);
+        const size_t blob_words = (size_t)((nbits + 15) / 16);
+        std::vector<uint16_t>& blk = blocks[(size_t)t];
+        blk.assign(blob_words, 0);
+        uint64_t pos = 0;
+        for (int32_t j = 0; j < nst; j++) {
+            const int e = state_exponent(x0[(size_t)j]);
+            put_bits(blk, 0, pos, x0[(size_t)j] - (1u << (16 + e)), 16 + e);
+            pos += 16 + e;
+        }
+        int32_t lmax = 0;
+        for (int32_t j = 0; j < nst; j++) {
+            const std::vector<uint16_t>& d = dec[(size_t)j];
+            const int32_t len = std::max((int32_t)d.size(), base);
+            blk.insert(blk.end(), d.begin(), d.end());
+            blk.resize(blk.size() + (size_t)(len - (int32_t)d.size()), 0);
+            E->slen[(size_t)(t * nst + j)] =
+                (uint8_t)((len - base) | state_exponent(x0[(size_t)j]) << 4);
+            lmax = std::max(lmax, len);
+        }
+        const size_t streams_end = blk.size();
         const size_t padded = (blk.size() + 1 + 7) & ~(size_t)7;
         if (padded > 65535) too_big[(size_t)t] = 1;
         blk.resize(padded, 0);
-        // stream lengths as the decoder stages them: up to the next state's
-        // start, the last one up to the end of the padded block
-        int32_t lmax = 0;
-        for (int32_t j = 0; j < nst; j++) {
-            const size_t sid = (size_t)(t * nst + j);
-            const int64_t end = j + 1 < nst ? E->soffs[sid + 1] : (int64_t)padded;
-            lmax = std::max<int32_t>(lmax, (int32_t)(end - E->soffs[sid]));
-        }
-        longest[(size_t)t] = lmax;
+        // the last stream as staged: up to the end of the padded block
+        const int32_t last = std::max((int32_t)dec[(size_t)nst - 1].size(), base);
+        longest[(size_t)t] = std::max(lmax, (int32_t)(padded - streams_end) + last);
+        E->tile_meta[(size_t)t] = (uint32_t)(base & 0xFF) | (uint32_t)blob_words << 16;
         // the tile's escapes in column order, rows ascending within a column
         for (int32_t c = 0; c < C; c++)
             for (int32_t r = 0; r < R; r++) {
@@ -308,7 +347,7 @@ extern "C" int rans_w64_encode(const int32_t* codes, int32_t rows, int32_t cols,
 }
 
 extern "C" int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* tile_off,
-                                     uint8_t* slen, uint32_t* states, uint32_t* table,
+                                     uint32_t* tile_meta, uint8_t* slen, uint32_t* table,
                                      int64_t* freq, int32_t* esc_tileptr, uint16_t* esc_pos,
                                      int16_t* esc_val) {
     if (!handle) return RANS_EARG;
@@ -318,8 +357,8 @@ extern "C" int rans_w64_encode_fetch(void* handle, uint16_t* words, uint32_t* ti
     };
     put(words, E->words);
     put(tile_off, E->tile_off);
+    put(tile_meta, E->tile_meta);
     put(slen, E->slen);
-    put(states, E->states);
     put(esc_tileptr, E->esc_tileptr);
     put(esc_pos, E->esc_pos);
     put(esc_val, E->esc_val);
@@ -337,7 +376,7 @@ extern "C" int rans_w64_encode_counts(void* handle, int64_t* counts) {
 extern "C" void rans_w64_encode_free(void* handle) { delete static_cast<Encoded*>(handle); }
 
 extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
-    if (!m || !out || !m->words || !m->tile_off || !m->slen || !m->states || !m->table)
+    if (!m || !out || !m->words || !m->tile_off || !m->slen || !m->tile_meta || !m->table)
         return RANS_EARG;
     const int32_t rows = m->rows, cols = m->cols, R = m->R, C = m->C, S = m->S;
     if (R <= 0 || C <= 0 || S <= 0 || rows % R || cols % C || C % (64 * S)) return RANS_EGEOMETRY;
@@ -349,11 +388,23 @@ extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
     // tile-by-tile decode would return).
     auto decode_tile = [&](int64_t t) -> int {
         const int32_t rb = (int32_t)(t / ncb), cb = (int32_t)(t % ncb);
-        int64_t start = m->tile_off[t];  // streams follow each other in state order
+        const int64_t blk = m->tile_off[t], blk_end = m->tile_off[t + 1];
+        const int32_t base = (int32_t)(m->tile_meta[t] & 0xFF);
+        const int64_t blob_words = m->tile_meta[t] >> 16;
+        if (blk_end < blk || blk + blob_words > blk_end || blk_end > nwords) return RANS_EARG;
+        // the initial states' mantissas, then the streams in state order
+        uint64_t bit = 0;
+        int64_t start = blk + blob_words;
         for (int32_t j = 0; j < nst; j++) {
             const int32_t s = j / 64, l = j % 64;
             const int64_t sid = t * nst + j;
-            uint32_t st = m->states[sid];
+            const int32_t e = m->slen[sid] >> 4, nb = 16 + e;
+            if (bit + (uint64_t)nb > (uint64_t)blob_words * 16) return RANS_EARG;
+            uint32_t mant = 0;
+            for (int i = 0; i < nb; i++, bit++)
+                mant |= (uint32_t)((m->words[blk + (int64_t)(bit >> 4)] >> (bit & 15)) & 1u) << i;
+            uint32_t st = (1u << nb) | mant;
+            const int64_t len = base + (m->slen[sid] & 15);
             int64_t p = start;
             for (int32_t k = 0; k < nk; k++) {
                 const int64_t col = (int64_t)cb * C + 64 * ((int64_t)S * k + s) + l;
@@ -361,18 +412,19 @@ extern "C" int rans_w64_decode_host(const rans_w64_matrix* m, int32_t* out) {
                     const uint32_t e = m->table[st & (kM - 1)];
                     st = ((e >> 8) & 0xFFFu) * (st >> kScaleBits) + (e >> 20);
                     if (st < kRansL) {
-                        if (p >= nwords) return RANS_EARG;
+                        if (p >= start + len) return RANS_EARG;
                         st = (st << 16) | m->words[p++];
                     }
                     out[((int64_t)rb * R + r) * cols + col] = (int32_t)(e & 0xFF) - 128;
                 }
             }
             if (st != kRansL) return (int)(sid + 1 > 0x7fffffff ? 0x7fffffff : sid + 1);
-            // the state consumed exactly its stored length
-            if (p - start != m->slen[sid]) return RANS_EARG;
-            start = p;
+            // the state consumed exactly its stored length, or stopped short of
+            // a stream padded up to its tile's base
+            if (p - start != len && len != base) return RANS_EARG;
+            start += len;
         }
-        return 0;
+        return start < blk_end ? 0 : RANS_EARG;  // at least one pad word follows
     };
     std::vector<int> err((size_t)ntiles, 0);
     const int nth = (int)std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency()));

@@ -65,7 +65,7 @@ class RansMatrixDesc(ctypes.Structure):
                 ("max_tile_words", ctypes.c_int32), ("max_state_words", ctypes.c_int32),
                 ("flags", ctypes.c_int32),
                 ("words", ctypes.c_void_p), ("tile_off", ctypes.c_void_p),
-                ("slen", ctypes.c_void_p), ("states", ctypes.c_void_p),
+                ("slen", ctypes.c_void_p), ("tile_meta", ctypes.c_void_p),
                 ("table", ctypes.c_void_p), ("table_lds", ctypes.c_void_p),
                 ("esc_tileptr", ctypes.c_void_p),
                 ("esc_pos", ctypes.c_void_p), ("esc_val", ctypes.c_void_p),
@@ -281,18 +281,50 @@ def w64_tiling(rows, cols, R, C, S=None):
     raise AssertionError(f"no legal w64 tiling for R={R}, C={C}, S={S}")
 
 
+def stream_lengths(enc):
+    """Stored words of every state's stream (int64, one per state in state
+    order): its tile's base (tile_meta bits 0-7) plus the 4-bit delta in the
+    low half of its slen byte."""
+    ntiles = enc["tile_off"].size - 1
+    base = (enc["tile_meta"].astype(np.int64) & 0xFF)[:ntiles, None]
+    return (base + (enc["slen"].astype(np.int64).reshape(ntiles, -1) & 15)).reshape(-1)
+
+
 def stream_offsets(enc):
     """Start of every state's stream in enc["words"] (uint32 word offsets,
     one per state in state order): the counterpart of the reference's
-    per-lane ``offs`` (kernel/rans.py:86), derived from the tile offsets and
-    the per-state stream lengths the format stores instead."""
-    slen = enc["slen"].astype(np.int64)
+    per-lane ``offs`` (kernel/rans.py:86), derived from the tile offsets, the
+    tile's initial-state words and the per-state stream lengths the format
+    stores instead."""
     ntiles = enc["tile_off"].size - 1
     if ntiles == 0:
         return np.zeros(0, np.uint32)
-    per = slen.reshape(ntiles, -1)
-    start = enc["tile_off"][:-1].astype(np.int64)[:, None] + np.cumsum(per, axis=1) - per
+    per = stream_lengths(enc).reshape(ntiles, -1)
+    first = enc["tile_off"][:-1].astype(np.int64) + (enc["tile_meta"].astype(np.int64) >> 16)
+    start = first[:, None] + np.cumsum(per, axis=1) - per
     return start.reshape(-1).astype(np.uint32)
+
+
+def initial_states(enc):
+    """Every state's initial decoder value (uint32, state order), read back
+    from the format: exponent e in the high half of its slen byte, and its
+    16 + e bits below the leading one bit-packed at the start of its tile's
+    block, state after state (little-endian bit stream of the words)."""
+    ntiles = enc["tile_off"].size - 1
+    if ntiles == 0:
+        return np.zeros(0, np.uint32)
+    nst = enc["slen"].size // ntiles
+    e = (enc["slen"].astype(np.int64) >> 4).reshape(ntiles, nst)
+    nb = 16 + e
+    bit = np.cumsum(nb, axis=1) - nb  # within the tile's blob
+    words = np.asarray(enc["words"], np.uint16)
+    start = enc["tile_off"][:-1].astype(np.int64)[:, None] * 16 + bit  # absolute bit
+    x = np.zeros(start.shape, np.int64)
+    for i in range(31):  # at most 31 mantissa bits
+        b = start + i
+        v = (words[np.minimum(b >> 4, words.size - 1)].astype(np.int64) >> (b & 15)) & 1
+        x |= np.where(i < nb, v << i, 0)
+    return (x | (np.int64(1) << nb)).reshape(-1).astype(np.uint32)
 
 
 def encode(codes, R, C, S=None, threads=None):
@@ -304,8 +336,10 @@ def encode(codes, R, C, S=None, threads=None):
 
     Returns a dict with the reference's keys (words, offs, table, R, C,
     shape, bits_payload, bits_state_offs, bits_table, entropy_model,
-    rans.py:93-98) and the w64 stream: tile_off, slen, states, the escape
-    side table (esc_tileptr, esc_pos, esc_val), tile_R, tile_C, S,
+    rans.py:93-98) and the w64 stream: tile_off, tile_meta, slen (the
+    initial states sit bit-packed in the words; initial_states reads them
+    back), the escape side table (esc_tileptr, esc_pos, esc_val), tile_R,
+    tile_C, S,
     stream_cols, max_tile_words, max_state_words, bits_escape, and
     layout = "w64".  offs keeps the reference's meaning (each stream's first
     word) but there is one stream per 64-lane state, not per 32-lane lane:
@@ -314,8 +348,9 @@ def encode(codes, R, C, S=None, threads=None):
     the matrix's own; the stream holds stream_cols = w64_stream_cols(cols)
     columns (32 columns of code 0 appended when cols % 64 == 32).  Bit
     accounting, per weight of the matrix: bits_payload (renormalisation
-    words), bits_state_offs (initial states, per-state lengths, tile offsets
-    and tile padding), bits_table (16 KB table), bits_escape (side table);
+    words), bits_state_offs (initial states, per-state length and exponent
+    bytes, tile offsets and metadata, length and tile padding), bits_table
+    (16 KB table), bits_escape (side table);
     appended columns are paid for in these.  entropy_model is over the
     matrix's own codes."""
     codes = np.ascontiguousarray(codes, dtype=np.int32)
@@ -340,8 +375,8 @@ def encode(codes, R, C, S=None, threads=None):
         (int(v) for v in info)
     words = np.zeros(nwords, np.uint16)
     tile_off = np.zeros(ntiles + 1, np.uint32)
+    tile_meta = np.zeros(ntiles, np.uint32)
     slen = np.zeros(nstates, np.uint8)
-    states = np.zeros(nstates, np.uint32)
     table = np.zeros(M, np.uint32)
     freq = np.zeros(256, np.int64)
     esc_tileptr = np.zeros(ntiles + 1, np.int32)
@@ -349,7 +384,7 @@ def encode(codes, R, C, S=None, threads=None):
     esc_val = np.zeros(nesc, np.int16)
     counts = np.zeros(256, np.int64)
     try:
-        rc = lib.rans_w64_encode_fetch(h, _p(words), _p(tile_off), _p(slen), _p(states),
+        rc = lib.rans_w64_encode_fetch(h, _p(words), _p(tile_off), _p(tile_meta), _p(slen),
                                        _p(table), _p(freq), _p(esc_tileptr), _p(esc_pos),
                                        _p(esc_val))
         assert rc == 0
@@ -362,12 +397,12 @@ def encode(codes, R, C, S=None, threads=None):
     present = counts > 0
     entropy_model = float(-(counts[present] * np.log2(freq[present] / M)).sum() / N)
     pad_words = nwords - payload_words
-    enc = dict(words=words, tile_off=tile_off, slen=slen, states=states, table=table,
+    enc = dict(words=words, tile_off=tile_off, tile_meta=tile_meta, slen=slen, table=table,
                esc_tileptr=esc_tileptr, esc_pos=esc_pos, esc_val=esc_val,
                R=R, C=C, tile_R=tR, tile_C=tC, S=tS, shape=(rows, cols), stream_cols=scols,
                max_tile_words=max_tile_words, max_state_words=max_state_words,
                bits_payload=16 * payload_words / N,
-               bits_state_offs=(40 * nstates + 32 * (ntiles + 1) + 16 * pad_words) / N,
+               bits_state_offs=(8 * nstates + 32 * (2 * ntiles + 1) + 16 * pad_words) / N,
                bits_table=32 * M / N,
                bits_escape=(32 * (ntiles + 1) + 32 * nesc) / N,
                entropy_model=entropy_model, layout=LAYOUT_W64)
@@ -497,7 +532,8 @@ def pick_tiling(rows, cols, R=None, S=1, target_states=None, max_ncb=None, bits=
 def _host_desc(enc, keep):
     """rans_w64_matrix over host numpy arrays (for rans_w64_decode_host)."""
     arrs = {k: np.ascontiguousarray(enc[k]) for k in
-            ("words", "tile_off", "slen", "states", "table", "esc_tileptr", "esc_pos", "esc_val")}
+            ("words", "tile_off", "tile_meta", "slen", "table", "esc_tileptr", "esc_pos",
+             "esc_val")}
     keep.append(arrs)
     rows = enc["shape"][0]
     tR, tC, tS = tiling_of(enc)
@@ -578,7 +614,7 @@ class RansMatrix:
         self.words = up(enc["words"], np.int16)
         self.tile_off = up(enc["tile_off"], np.int32)
         self.slen = up(enc["slen"], np.uint8)
-        self.states = up(enc["states"], np.int32)
+        self.tile_meta = up(enc["tile_meta"], np.int32)
         # the kernels read the table's LDS image; the packed table is only
         # for the host decoder and stays on the host
         self.table_lds = up(table_lds(enc["table"], lib), np.int32)
@@ -600,7 +636,7 @@ class RansMatrix:
             flags=(int(flags) & (F_WORDS_MASK | F_TABLE8 | F_TABLE4)) |
             (0 if len(enc["esc_pos"]) else F_NO_ESCAPES),
             words=self.words.data_ptr(), tile_off=self.tile_off.data_ptr(),
-            slen=self.slen.data_ptr(), states=self.states.data_ptr(),
+            slen=self.slen.data_ptr(), tile_meta=self.tile_meta.data_ptr(),
             table=None, table_lds=self.table_lds.data_ptr(),
             esc_tileptr=self.esc_tileptr.data_ptr(),
             esc_pos=self.esc_pos.data_ptr(), esc_val=self.esc_val.data_ptr(),
@@ -616,7 +652,7 @@ class RansMatrix:
         # plus the 16 KB image of 4-byte entries where it is used)
         imgs = (self.table_lds,) if self.table_lds4 is None else (self.table_lds, self.table_lds4)
         self.nbytes = sum(t.numel() * t.element_size() for t in
-                          (self.words, self.tile_off, self.slen, self.states, *imgs,
+                          (self.words, self.tile_off, self.slen, self.tile_meta, *imgs,
                            self.esc_tileptr)) + 4 * int(len(enc["esc_pos"]))
 
     @property

@@ -9,12 +9,11 @@ Layout (all integers little endian, every section 64-byte aligned):
 
     header, 64 bytes
         magic      8 bytes  b"VRAMCW64"
-        version    u32      5 (written); 4 is also read: the same layout,
-                            whose record slot for the appended columns was
-                            zero padding in its first files, so they read
-                            as 0 appended columns (1 to 3 held a row-CSR
-                            side table, 16-bit stream offsets or a 32-bit
-                            side table; they are not read)
+        version    u32      6 (1 to 5 held earlier stream layouts and are
+                            not read: 4 and 5 a u32 initial state and a
+                            byte length per state, 1 to 3 a row-CSR side
+                            table, 16-bit stream offsets or a 32-bit side
+                            table; re-encode such a matrix)
         nmat       u32      number of matrices
         index_off  u64      byte offset of the index
         file_bytes u64      total file size (truncation check)
@@ -26,15 +25,16 @@ Layout (all integers little endian, every section 64-byte aligned):
                    R, C, S: the w64 tiling, tile_R/tile_C/S of the enc dict)
         nwords, ntiles, nstates, nesc, payload_words                  u64 x 5
         entropy_model                                                 f64
-        offsets of words, tile_off, slen, states, table, esc_tileptr,
-                   esc_pos, esc_val, step                             u64 x 9
+        offsets of words, tile_off, slen, tile_meta, table,
+                   esc_tileptr, esc_pos, esc_val, step                u64 x 9
         crc32 of the nine sections, in that order                     u32
         appended columns (0, or 32 when the matrix's cols % 64 == 32)  i32
-                   (new in version 5; version 4 files hold 0 here)
         zero padding to 256 bytes
     sections
-        words u16[nwords], tile_off u32[ntiles+1], slen u8[nstates],
-        states u32[nstates], table u32[4096] (reference packing),
+        words u16[nwords] (each tile's bit-packed initial states, then its
+        streams), tile_off u32[ntiles+1], slen u8[nstates] (length delta |
+        state exponent << 4), tile_meta u32[ntiles] (length base | blob
+        words << 16), table u32[4096] (reference packing),
         esc_tileptr i32[ntiles+1], esc_pos u16[nesc], esc_val i16[nesc],
         step f32[cols - appended columns]
 
@@ -51,14 +51,14 @@ import numpy as np
 import rans
 
 MAGIC = b"VRAMCW64"
-VERSION = 5
-READ_VERSIONS = (4, 5)
+VERSION = 6
+READ_VERSIONS = (6,)
 _HEADER = struct.Struct("<8sIIQQ32x")
 _RECORD = struct.Struct("<64s8i5Qd9QIi")
 RECORD_BYTES = 256
 ALIGN = 64
 _SECTIONS = (("words", np.uint16), ("tile_off", np.uint32), ("slen", np.uint8),
-             ("states", np.uint32), ("table", np.uint32), ("esc_tileptr", np.int32),
+             ("tile_meta", np.uint32), ("table", np.uint32), ("esc_tileptr", np.int32),
              ("esc_pos", np.uint16), ("esc_val", np.int16), ("step", np.float32))
 assert _HEADER.size == 64 and _RECORD.size <= RECORD_BYTES
 
@@ -69,7 +69,7 @@ def _align(n):
 
 def _section_lengths(cols, nwords, ntiles, nstates, nesc):
     """Entries of each section; cols: the matrix's own columns (step)."""
-    return dict(words=nwords, tile_off=ntiles + 1, slen=nstates, states=nstates,
+    return dict(words=nwords, tile_off=ntiles + 1, slen=nstates, tile_meta=ntiles,
                 table=rans.M, esc_tileptr=ntiles + 1, esc_pos=nesc, esc_val=nesc, step=cols)
 
 
@@ -89,7 +89,7 @@ def save(path, entries):
             a = e["step"] if key == "step" else enc[key]
             arrays[key] = np.ascontiguousarray(np.asarray(a).reshape(-1), dtype=dt)
         n = _section_lengths(cols, arrays["words"].size, arrays["tile_off"].size - 1,
-                             arrays["states"].size, arrays["esc_pos"].size)
+                             arrays["slen"].size, arrays["esc_pos"].size)
         for key, _ in _SECTIONS:
             assert arrays[key].size == n[key], f"{e['name']}: {key} has {arrays[key].size} " \
                                                f"entries, expected {n[key]}"
@@ -106,7 +106,7 @@ def save(path, entries):
         recs.append(_RECORD.pack(name, rows, scols, *rans.tiling_of(enc),
                                  enc["max_tile_words"], enc["max_state_words"],
                                  int(e.get("flags", 0)), arrays["words"].size,
-                                 arrays["tile_off"].size - 1, arrays["states"].size,
+                                 arrays["tile_off"].size - 1, arrays["slen"].size,
                                  arrays["esc_pos"].size, payload_words,
                                  float(enc.get("entropy_model", 0.0)), *offs, crc,
                                  scols - cols))
@@ -179,13 +179,13 @@ def load(path, verify=True, mmap=True):
         N = rows * cols
         pad = nwords - payload_words
         enc = dict(words=arrays["words"], tile_off=arrays["tile_off"], slen=arrays["slen"],
-                   states=arrays["states"], table=arrays["table"],
+                   tile_meta=arrays["tile_meta"], table=arrays["table"],
                    esc_tileptr=arrays["esc_tileptr"], esc_pos=arrays["esc_pos"],
                    esc_val=arrays["esc_val"], R=R, C=C, tile_R=R, tile_C=C, S=S,
                    shape=(rows, cols), stream_cols=scols,
                    max_tile_words=mtw, max_state_words=msw,
                    bits_payload=16 * payload_words / N,
-                   bits_state_offs=(40 * nstates + 32 * (ntiles + 1) + 16 * pad) / N,
+                   bits_state_offs=(8 * nstates + 32 * (2 * ntiles + 1) + 16 * pad) / N,
                    bits_table=32 * rans.M / N,
                    bits_escape=(32 * (ntiles + 1) + 32 * nesc) / N,
                    entropy_model=entropy_model, layout=rans.LAYOUT_W64)
