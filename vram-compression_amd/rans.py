@@ -469,8 +469,9 @@ def pick_tiling(rows, cols, R=None, S=1, target_states=None, max_ncb=None, bits=
       the launch is latency-bound far above its byte count (1536x1536 at
       3.25 bits: 5.5 us with 49152 states, 8.1 us with 36864, +0.21
       bits/weight); matrices above 32M weights use about 160 symbols per
-      state.  Fewer states cost less per-state overhead (40 bits each),
-      more states give more parallelism.
+      state.  Fewer states cost less per-state overhead (a byte of length
+      and exponent plus a 16 to 31-bit mantissa, ~26 bits beyond the
+      entropy each), more states give more parallelism.
     - column tiles per tile row (ncb): 8 is best (8 waves of a workgroup
       share one LDS table, so more waves fit per CU), then 4-7 and 16 (the
       latter needs the split-K reduction); fewer than 4 repeat the table
