@@ -467,11 +467,24 @@ def qwen15b_layer_shapes():
             ("gate", 8960, 1536), ("up", 8960, 1536), ("down", 1536, 8960)]
 
 
+# Tilings of the per-token chain that spend its bits on more states where a
+# launch is short, measured on MI355X (rotated copies, 3.25 bits, µs per
+# launch, with compact state metadata):
+# - o, 1536x1536: 3x512 5.16 at 4.46 bits/weight, against pick_tiling's 8x384
+#   6.35 at 3.91 (3x384: 4.95 at 4.83);
+# - down, 1536x8960: 3x1792 as the headline (3.4% faster than 3x2240);
+# - the q/k/v group (2048 rows): 8x256, 1536 waves, against 16x256's 768.
+# The whole chain then takes 993 us per token at 3.646 bits/weight against
+# 1082 us at 3.573 with pick_tiling's tilings (one box, two runs each); the
+# next denser choice (o 3x384) passes 3.66 bits.
+CHAIN_TILING = {(1536, 1536): (3, 512), (1536, 8960): (3, 1792)}
+CHAIN_GROUP_TILING = {"qkv": (8, 256)}
+
+
 def chain_tiling(rows, cols):
-    """Tiling for one matrix of the per-token chain: the library's default
-    (about 105 symbols per state on large matrices, at least 768 waves on
-    small ones)."""
-    return pick_tiling(rows, cols, S=1)
+    """Tiling for one matrix of the per-token chain: CHAIN_TILING's for the
+    shapes it measured, else the library's default (pick_tiling)."""
+    return CHAIN_TILING.get((rows, cols)) or pick_tiling(rows, cols, S=1)
 
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak
@@ -550,7 +563,7 @@ def config_matrix(rows, cols, bits, dist, escape_frac, batch, seed, lib, R=None,
 CHAIN_GROUPS = {"q": "qkv", "k": "qkv", "v": "qkv", "gate": "mlp", "up": "mlp"}
 
 
-def build_chain(bits=3.25, layers=28, seed=0, grouped=False, batch=1, tune=True,
+def build_chain(bits=3.25, layers=28, seed=0, grouped=False, batch=1, tune=False,
                 keep_codes=False, bf16=True, lib=None):
     """The per-token chain's weight set: 7*layers matrices over a
     random-init Qwen2.5-1.5B-shaped model (one table per matrix, ECSQ-like
@@ -558,8 +571,12 @@ def build_chain(bits=3.25, layers=28, seed=0, grouped=False, batch=1, tune=True,
     uploaded, and its launch sequence.
 
     grouped: q, k, v and gate, up of a layer are tiled for one grouped
-    launch each (pick_group_tiling).  tune: the word-fetch policy is timed
-    once per shape, on the first layer.  keep_codes: keep each matrix's
+    launch each (CHAIN_GROUP_TILING, else pick_group_tiling).  tune: the
+    word-fetch policy is timed once per shape, on the first layer
+    (RansMatrix.tune, hot launches of one copy); off by default, since the
+    library's policy was chosen on cold copies and the chain reads its
+    weights cold (on o in 8x384 tiles tune picked "always", 7.2 us cold
+    against "refill"'s 6.35).  keep_codes: keep each matrix's
     codes and step on the host (for a parity check).  bf16: also build the
     bf16 weights of the comparator chain.
 
@@ -577,7 +594,8 @@ def build_chain(bits=3.25, layers=28, seed=0, grouped=False, batch=1, tune=True,
     if grouped:
         for g in set(CHAIN_GROUPS.values()):
             members = [(n, r, c) for n, r, c in shapes if CHAIN_GROUPS.get(n) == g]
-            t = pick_group_tiling([r for _, r, _ in members], members[0][2])
+            t = CHAIN_GROUP_TILING.get(g) or \
+                pick_group_tiling([r for _, r, _ in members], members[0][2])
             for n, _, _ in members:
                 tiling[n] = t
     # one step per shape, chosen on a sample, so every layer has ~`bits` bits
