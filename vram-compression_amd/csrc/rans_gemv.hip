@@ -40,6 +40,9 @@ namespace {
 constexpr uint32_t kProbM = 4096;
 constexpr uint32_t kRansL = 1u << 16;
 constexpr int kMaxWaves = 8;
+// Waves of a workgroup that takes two tile rows (up to five column tiles per
+// row); its launch bound allows three waves per SIMD.
+constexpr int kMaxWavesRows2 = 10;
 
 // Table entry in LDS, in one of two layouts:
 //   - 8 bytes {freq | code<<24, slot - cum} (T4 = false): one mad consumes
@@ -61,9 +64,10 @@ constexpr int gemv_max_batch(int R) { return R <= 8 ? 8 : 4; }
 // arrays (their offsets are compile-time constants, so table addressing
 // needs no base add); the per-wave regions are dynamic.  The GEMV's
 // reduction scratch holds R*B floats per wave: the host reserves it for the
-// largest batch compiled for R, plus the 16-byte arrival flag.
+// largest batch compiled for R and the largest (two-row) workgroup, plus the
+// 16-byte arrival flag.
 constexpr int gemv_static_lds(int R, bool t4 = false) {
-    return (t4 ? 4 : 8) * (int)kProbM + 4 * kMaxWaves * R * gemv_max_batch(R) + 16;
+    return (t4 ? 4 : 8) * (int)kProbM + 4 * kMaxWavesRows2 * R * gemv_max_batch(R) + 16;
 }
 constexpr int kDecodeStaticLds = (int)sizeof(TabEntry<false>) * (int)kProbM;
 constexpr int kLdsMax = 160 * 1024;
@@ -472,11 +476,11 @@ template <int R, int B>
 constexpr int kMinWavesPerEu = ((R == 20 && B == 4) || (R == 8 && B == 8)) ? 4 : 1;
 
 template <int R, int S, int B, bool XBF16, bool REFILL, bool GROUP, bool T4, bool ROWS2>
-__global__ void __launch_bounds__(64 * kMaxWaves)
+__global__ void __launch_bounds__(64 * (ROWS2 ? kMaxWavesRows2 : kMaxWaves))
     __attribute__((amdgpu_waves_per_eu(kMinWavesPerEu<R, B>)))
     rans_w64_gemv_kernel(GemvArgs a) {
     __shared__ __align__(16) TabEntry<T4> tab[kProbM];
-    __shared__ float red[kMaxWaves * R * B];
+    __shared__ float red[(ROWS2 ? kMaxWavesRows2 : kMaxWaves) * R * B];
     __shared__ int flag[4];
     extern __shared__ __align__(16) uint16_t dyn[];
     constexpr int nst = 64 * S;
@@ -1425,11 +1429,12 @@ int device_cus() {
 // Whether a launch takes two tile rows per workgroup.  The 32 KB table copy
 // of each workgroup sits on the critical path of a launch the chip holds at
 // once (copying it twice made 1536x8960 6% slower); two rows per workgroup
-// halve the copies (1536x8960: 1.3-2.8% faster over two boxes, 1536x8960 at
-// 2.25 bits with escapes 5%).  Only while the halved grid still gives
+// halve the copies (1536x8960 in 3x2240 tiles: 1.3-2.8% faster over two
+// boxes, at 2.25 bits with escapes 5%; in 3x1792 tiles, two rows of five
+// waves: 10.05 -> 9.88 us).  Only while the halved grid still gives
 // every CU a workgroup: 1536x1536 in 8x384 tiles (192 workgroups) ran 3-5%
 // slower as 96.  Single-matrix launches with one state per lane, one
-// workgroup per tile row (no split-K), at most 4 waves per row, an even
+// workgroup per tile row (no split-K), at most 5 waves per row, an even
 // number of tile rows and the 8-byte table entries; not tiles taller than
 // 16 rows.  The paired workgroup holds both rows' staged blocks, so it is
 // only taken when twice the dynamic LDS (lds bytes for one row's waves)
@@ -1437,7 +1442,7 @@ int device_cus() {
 bool use_rows2(const rans_w64_matrix* m, int n, int v, int waves, int ngroups, int grid,
                size_t lds) {
     if (n != 1 || m->S != 1 || (v & 8) || m->R > 16 || ngroups != 1) return false;
-    if (2 * waves > kMaxWaves || (m->rows / m->R) % 2) return false;
+    if (2 * waves > kMaxWavesRows2 || (m->rows / m->R) % 2) return false;
     if (2 * lds + gemv_static_lds(m->R) > (size_t)kLdsMax) return false;
     const int cus = device_cus();
     return cus > 0 && grid >= 2 * cus;
