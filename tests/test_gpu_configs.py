@@ -188,8 +188,9 @@ def test_paired_rows_need_lds_for_both(rans, lib, dev):
 
 def test_paired_rows_query(rans, lib, dev):
     """rans_gemv_rows2 says which launches pair tile rows: 1536x8960 in
-    3x2240 tiles (512 tile rows, two per CU) does at batch 1 and 4; with the
-    4-byte table entries forced, or at S = 2, it does not."""
+    3x2240 tiles (512 tile rows, two per CU) does at batch 1 and 4, and in
+    3x1792 tiles at batch 1; with the 4-byte table entries forced, or at
+    S = 2, it does not."""
     import rans_bench as B
     print("case paired rows query", flush=True)
     codes = B.synth_codes_full(1536, 8960, 3.25, seed=3)
@@ -197,6 +198,9 @@ def test_paired_rows_query(rans, lib, dev):
     m = rans.RansMatrix(rans.encode(codes, 3, 2240, 1), step, lib)
     for batch in (1, 4):
         assert lib.rans_gemv_rows2(ctypes.byref(m._desc), rans.X_BF16, batch) == 1
+    # five column tiles per row: workgroups of 10 waves
+    m5 = rans.RansMatrix(rans.encode(codes, 3, 1792, 1), step, lib)
+    assert lib.rans_gemv_rows2(ctypes.byref(m5._desc), rans.X_BF16, 1) == 1
     m4 = rans.RansMatrix(rans.encode(codes, 3, 2240, 1), step, lib, flags=rans.F_TABLE4)
     assert lib.rans_gemv_rows2(ctypes.byref(m4._desc), rans.X_BF16, 1) == 0
     m2 = rans.RansMatrix(rans.encode(codes, 3, 1792, 2), step, lib)

@@ -635,18 +635,20 @@ def test_escape_value_extremes(rans, oracle, lib, dev, R, C):
 
 
 @pytest.mark.parametrize("tile_rows", [513, 514])
-def test_two_tile_rows_odd_and_even(rans, oracle, lib, dev, tile_rows):
+@pytest.mark.parametrize("C", [2240, 1792])
+def test_two_tile_rows_odd_and_even(rans, oracle, lib, dev, tile_rows, C):
     """A grid of at least twice the CUs pairs tile rows only when their
-    count is even: 513 tile rows of 3x2240 tiles keep one row per
-    workgroup, 514 pair them.  Both agree with the one-row launch (forced
+    count is even: 513 tile rows of 3x2240 or 3x1792 tiles keep one row per
+    workgroup, 514 pair them (8 waves per workgroup for four column tiles
+    per row, 10 for five).  Both agree with the one-row launch (forced
     through the 4-byte table entries) bit for bit, and with the oracle."""
     import rans_bench as B
     rows, cols = 3 * tile_rows, 8960
-    print(f"case tile rows {tile_rows}", flush=True)
+    print(f"case tile rows {tile_rows} C={C}", flush=True)
     codes = B.synth_codes_full(rows, cols, 3.25, dist="laplace", seed=tile_rows)
     codes[rows - 1, cols - 1] = 900  # an escape in the last tile row
     step = torch.from_numpy(B.lognormal_steps(cols, seed=tile_rows))
-    enc = rans.encode(codes, 3, 2240, 1)
+    enc = rans.encode(codes, 3, C, 1)
     m = rans.RansMatrix(enc, step, lib)
     m1 = rans.RansMatrix(enc, step, lib, flags=rans.F_TABLE4)
     # the library's own answer: paired for the even count only
