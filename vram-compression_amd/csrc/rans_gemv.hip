@@ -1432,8 +1432,11 @@ int device_cus() {
 // halve the copies (1536x8960 in 3x2240 tiles: 1.3-2.8% faster over two
 // boxes, at 2.25 bits with escapes 5%; in 3x1792 tiles, two rows of five
 // waves: 10.05 -> 9.88 us).  Only while the halved grid still gives
-// every CU a workgroup: 1536x1536 in 8x384 tiles (192 workgroups) ran 3-5%
-// slower as 96.  Single-matrix launches with one state per lane, one
+// every CU a workgroup (1536x1536 in 8x384 tiles, 192 workgroups, ran 3-5%
+// slower as 96), and only where pairing does not raise the most waves a CU
+// holds when the workgroups spread evenly: 5120x5120 in 8x1024 tiles (640
+// workgroups of 5 waves, 15 waves on the busiest CU) ran 14.5 -> 17.6 us as
+// 320 pairs (20).  Single-matrix launches with one state per lane, one
 // workgroup per tile row (no split-K), at most 5 waves per row, an even
 // number of tile rows and the 8-byte table entries; not tiles taller than
 // 16 rows.  The paired workgroup holds both rows' staged blocks, so it is
@@ -1445,7 +1448,10 @@ bool use_rows2(const rans_w64_matrix* m, int n, int v, int waves, int ngroups, i
     if (2 * waves > kMaxWavesRows2 || (m->rows / m->R) % 2) return false;
     if (2 * lds + gemv_static_lds(m->R) > (size_t)kLdsMax) return false;
     const int cus = device_cus();
-    return cus > 0 && grid >= 2 * cus;
+    if (cus <= 0 || grid < 2 * cus) return false;
+    const int64_t one = (int64_t)(grid + cus - 1) / cus * waves;
+    const int64_t two = (int64_t)(grid / 2 + cus - 1) / cus * 2 * waves;
+    return two <= one;
 }
 
 // Whether a single-matrix launch of the batch-B kernel runs with the 4-byte
