@@ -43,6 +43,8 @@ constexpr int kMaxWaves = 8;
 // Waves of a workgroup that takes two tile rows (up to five column tiles per
 // row); its launch bound allows three waves per SIMD.
 constexpr int kMaxWavesRows2 = 10;
+// Waves of a decode workgroup (tiles are taken linearly, any count works).
+constexpr int kMaxDecodeWaves = 10;
 
 // Table entry in LDS, in one of two layouts:
 //   - 8 bytes {freq | code<<24, slot - cum} (T4 = false): one mad consumes
@@ -847,7 +849,7 @@ __device__ __forceinline__ uint16_t to_bf16(float f) { return __builtin_bit_cast
 // stores have completed, each wave overwrites the escape positions of its
 // tile (decoded as 0) with their side-table values, so no second launch.
 template <int R, int S, int MODE>
-__global__ void __launch_bounds__(64 * kMaxWaves) rans_w64_decode_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(64 * kMaxDecodeWaves) rans_w64_decode_kernel(DecodeArgs a) {
     __shared__ __align__(16) TabEntry<false> tab[kProbM];
     extern __shared__ __align__(16) uint16_t dyn[];
     constexpr int nst = 64 * S;
@@ -1251,11 +1253,24 @@ int gemv_waves(const rans_w64_matrix* m) {
     return 0;
 }
 
+int device_cus();
+
+// Waves per decode workgroup: among the counts whose LDS fits, the one that
+// puts the fewest waves on the busiest CU when the workgroups spread evenly
+// over the CUs, the largest such (fewer table copies).
 int decode_waves(const rans_w64_matrix* m) {
     const WaveLayout L = wave_layout(m);
-    for (int w = 4; w >= 1; w >>= 1)
-        if (lds_bytes(w, L) + kDecodeStaticLds <= (size_t)kLdsMax) return w;
-    return 0;
+    const int64_t ntiles = (int64_t)(m->rows / m->R) * (m->cols / m->C);
+    const int cus = device_cus();
+    int best = 0;
+    int64_t best_load = 0;
+    for (int w = 1; w <= kMaxDecodeWaves; w++) {
+        if (lds_bytes(w, L) + kDecodeStaticLds > (size_t)kLdsMax) break;
+        const int64_t grid = (ntiles + w - 1) / w;
+        const int64_t load = cus > 0 ? (grid + cus - 1) / cus * w : -w;
+        if (!best || load <= best_load) best = w, best_load = load;
+    }
+    return best;
 }
 
 size_t counters_bytes(const rans_w64_matrix* m) {
