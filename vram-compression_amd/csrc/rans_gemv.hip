@@ -527,6 +527,13 @@ __global__ void __launch_bounds__(64 * (ROWS2 ? kMaxWavesRows2 : kMaxWaves))
     // This tile's range of the escape side table (lanes 0, 1), also needed early.
     const int tp = m.esc_tileptr[t + min(lane, 1)];
     asm volatile("" ::: "memory");  // keep these two loads first
+    // The kernels for launches that put several workgroups on a CU (the
+    // 4-byte table entries, chosen where the grid exceeds what the chip
+    // holds, and tiles of 20 or more rows) start the table copy while the
+    // tile extent is on its way; the others request the block copy first,
+    // so that it does not queue behind the table.
+    constexpr bool kTableFirst = T4 || R >= 20;
+    if constexpr (kTableFirst) stage_table(tab, m.table_lds, wave, W, lane);
     const uint32_t tmv = m.tile_meta[t];
     uint32_t len0[S];
 #pragma unroll
@@ -584,7 +591,7 @@ __global__ void __launch_bounds__(64 * (ROWS2 ? kMaxWavesRows2 : kMaxWaves))
     const int e_hi = esc ? __builtin_amdgcn_readlane(tp, 1) : 0;
     asm volatile("" ::"s"(e_lo), "s"(e_hi));
     stage_tile(raw, m.words, o0, n16, lane);
-    stage_table(tab, m.table_lds, wave, W, lane);
+    if constexpr (!kTableFirst) stage_table(tab, m.table_lds, wave, W, lane);
     constexpr int P = 2;  // chunks per wave prefetched: 128 escapes per tile
     const int cbase = cb * m.C;
     // tile column of an entry, clamped into the tile so that no side-table
