@@ -529,10 +529,11 @@ __global__ void __launch_bounds__(64 * (ROWS2 ? kMaxWavesRows2 : kMaxWaves))
     asm volatile("" ::: "memory");  // keep these two loads first
     // The kernels for launches that put several workgroups on a CU (the
     // 4-byte table entries, chosen where the grid exceeds what the chip
-    // holds, and tiles of 20 or more rows) start the table copy while the
-    // tile extent is on its way; the others request the block copy first,
-    // so that it does not queue behind the table.
-    constexpr bool kTableFirst = T4 || R >= 20;
+    // holds, tiles of 20 or more rows, and the batch kernels outside paired
+    // rows) start the table copy while the tile extent is on its way; the
+    // others request the block copy first, so that it does not queue behind
+    // the table.
+    constexpr bool kTableFirst = T4 || R >= 20 || (B >= 4 && !ROWS2);
     if constexpr (kTableFirst) stage_table(tab, m.table_lds, wave, W, lane);
     const uint32_t tmv = m.tile_meta[t];
     uint32_t len0[S];
