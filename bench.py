@@ -57,8 +57,8 @@ DEFAULT_TILING = (3, 1792, 1)
 # profiles/rans_w64_gemv_1536x8960_3.25b.md.  Keyed by (R, C, S, word fetch)
 # and by the hash of the library sources they were measured on
 # (library_source_hash): with other sources the line reports traffic null.
-PMC_TRAFFIC_KIB = {(3, 1792, 1, "refill"): dict(source_hash="8d8ca30a5844", commit="a9a6337",
-                                                fetch_kib=3451.6, write_kib=12.0)}
+PMC_TRAFFIC_KIB = {(3, 1792, 1, "refill"): dict(source_hash="921d6e673b83", commit="e180c16",
+                                                fetch_kib=3443.6, write_kib=12.0)}
 PMC_FETCH_FACTOR, PMC_WRITE_FACTOR = 2.0, 1.0
 
 
