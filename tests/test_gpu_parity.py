@@ -659,10 +659,14 @@ def test_two_tile_rows_odd_and_even(rans, oracle, lib, dev, tile_rows, C):
         want = 1 if tile_rows == 512 else 0
         assert lib.rans_gemv_rows2(ctypes.byref(m._desc), rans.X_BF16, 1) == want
     assert lib.rans_gemv_rows2(ctypes.byref(m1._desc), rans.X_BF16, 1) == 0
-    for batch in (1, 4):
+    for batch in (1, 4, 8):
         x = torch.randn(batch, cols, device="cuda").bfloat16()
         y = m.gemv(x).cpu()
-        assert torch.equal(y, m1.gemv(x).cpu())
+        # batch 8: the batch-8 kernel (paired rows too) against one-vector
+        # launches of the one-row kernel, which sum in the same order
+        y1 = m1.gemv(x).cpu() if batch < 8 else \
+            torch.cat([m1.gemv(x[i:i + 1]).cpu() for i in range(batch)])
+        assert torch.equal(y, y1)
         ref = oracle.gemv_f64(codes, x.float().cpu().numpy().astype(np.float64),
                               step.numpy().astype(np.float64))
         assert _rel_l2(y.numpy(), ref) <= REL_L2
